@@ -1,0 +1,33 @@
+"""CPU oracle for the FP8 hot path (test infrastructure only).
+
+This package restates, in numpy, the arithmetic of the reference's FP8 hot path so
+that the HIP implementation can be checked against it.  It is NOT part of the
+product: only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg
+of ``bench.py`` may import it, and only as the checker / the timed CPU baseline.
+The product path (``minimaxh3_amd``) never imports it and has no CPU fallback.
+
+Modules
+-------
+numerics   OCP float8 e4m3fn encode/decode and bf16 rounding (own integer/float64
+           implementations; pinned against torch's CPU casts in the tests).
+linear     quantize_rows, the row-wise scaled FP8 GEMM with bias, the LoRA branch
+           and GELU-tanh (kernels/fp8_linear.py:8-55, 87-108).
+attention  Q/K/V quantizers and the FP8 flash-attention forward algorithm
+           (kernels/fp8_attention.py:39-170, 185-297, 300-403).
+
+Pinning (what each function is checked against, see tests/test_oracle_*.py)
+--------------------------------------------------------------------------
+* e4m3 encode/decode, bf16 rounding: torch CPU ``.to(torch.float8_e4m3fn)`` /
+  ``.to(torch.bfloat16)`` on structured and random values, plus known answers.
+* quantize_rows / attention quantizers: closed forms (all-zero rows, the amax
+  element mapping to 0x7E/0xFE, ties), and an independent torch CPU restatement.
+* scaled GEMM: brute-force triple loop on tiny non-square shapes.
+* GELU-tanh: ``torch.nn.functional.gelu(approximate="tanh")``.
+* LoRA branch: torch CPU bf16 matmuls.
+* attention forward: tau=0 reduces to exact softmax attention (torch SDPA on the
+  dequantized inputs); q=0 gives the mean of V; a hand-computed two-tile case
+  pins the visit order and the lazy-max policy; Mitchell's closed form for the
+  exp2-free P codes; fully-masked rows give 0; a scalar brute-force loop.
+Nothing here is "parity unpinned" except the reduction order of fp32 sums
+(GEMM accumulation, the key mean), which the reference does not fix either.
+"""

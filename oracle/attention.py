@@ -1,0 +1,211 @@
+"""Oracle for the FP8 attention path (test infrastructure only).
+
+Restates kernels/fp8_attention.py of the reference:
+* ``quantize_q``    <- _quantize_q_kernel                (fp8_attention.py:39-77, launch 315-336)
+* ``key_mean``      <- k.float().mean(dim=2)              (fp8_attention.py:338)
+* ``quantize_k``    <- _quantize_k_kernel                (fp8_attention.py:80-119)
+* ``quantize_v``    <- _quantize_v_kernel                (fp8_attention.py:122-170)
+* ``attn_fwd``      <- _fp8_attn_kernel with BLOCK_N=128 (fp8_attention.py:185-297)
+* ``fp8_attention`` <- fp8_attention                     (fp8_attention.py:300-403)
+
+Layouts follow the reference: Q8/K8 [B,H,S,D] codes, V8T [B,H,D,Sk] codes (V
+transposed), per-128-row scales sQ [B,H,ceil(Sq/128)], sK [B,H,ceil(Sk/128)],
+per-channel sV [B,H,D].  All arithmetic that the reference does in fp32 is done in
+fp32 here; sums whose order the reference leaves to the compiler (the QK^T and PV
+contractions, row sums, the key mean) are done in float64 and rounded once.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .numerics import E4M3_MAX, bf16_round, e4m3_decode, e4m3_encode
+
+F32 = np.float32
+LOG2E = 1.4426950408889634
+BLOCK_M = 128
+NEG = F32(-1.0e9)
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _blockwise_quant(t, valid_rows, block):
+    """Shared body of the Q and K quantizers: one fp32 scale per `block` rows.
+
+    t: [B,H,S,D] fp32 (already multiplied by c / centred), rows >= valid_rows ignored.
+    scale = max(max|t| over the block, 1e-12) / 448; code = e4m3(clamp(t/scale)).
+    """
+    B, H, S, D = t.shape
+    nb = _cdiv(S, block)
+    pad = nb * block - S
+    tp = np.concatenate([t, np.zeros((B, H, pad, D), F32)], axis=2) if pad else t
+    tb = tp.reshape(B, H, nb, block, D)
+    amax = np.max(np.abs(tb), axis=(3, 4))
+    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    q = (tb / scale[..., None, None]).astype(F32)
+    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
+    codes = e4m3_encode(q).reshape(B, H, nb * block, D)[:, :, :S]
+    return codes, scale
+
+
+def quantize_q(q, c):
+    """fp8_attention.py:54-77: q~ = fp32(q) * c, per (b,h,128-row block) scale, codes.
+
+    c = (scale or 1/sqrt(D)) * log2(e) is applied in fp32 (line 69, c from line 315).
+    Returns (Q8 uint8 [B,H,Sq,D], sQ fp32 [B,H,ceil(Sq/128)]).
+    """
+    qt = (np.asarray(q, F32) * F32(c)).astype(F32)
+    return _blockwise_quant(qt, q.shape[2], BLOCK_M)
+
+
+def key_mean(k):
+    """fp8_attention.py:338: mean over the key axis in fp32 (float64 sum, rounded once)."""
+    return np.mean(np.asarray(k, np.float64), axis=2, keepdims=True).astype(F32)
+
+
+def quantize_k(k, mu):
+    """fp8_attention.py:95-119: k~ = fp32(k) - mu, per (b,h,128-key block) scale, codes.
+
+    Returns (K8 uint8 [B,H,Sk,D], sK fp32 [B,H,ceil(Sk/128)]).
+    """
+    kt = (np.asarray(k, F32) - np.asarray(mu, F32)).astype(F32)
+    return _blockwise_quant(kt, k.shape[2], 128)
+
+
+def quantize_v(v):
+    """fp8_attention.py:136-170: per-channel scale over all keys, codes stored transposed.
+
+    sV[b,h,d] = max(max_s |v|, 1e-12) / 448 ; V8T[b,h,d,s] = e4m3(clamp(v[b,h,s,d] / sV)).
+    Returns (V8T uint8 [B,H,D,Sk], sV fp32 [B,H,D]).
+    """
+    v = np.asarray(v, F32)
+    amax = np.max(np.abs(v), axis=2)
+    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    q = (v / scale[:, :, None, :]).astype(F32)
+    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
+    return np.ascontiguousarray(e4m3_encode(q).transpose(0, 1, 3, 2)), scale
+
+
+def p_codes(s, m, valid):
+    """The exp2-free P codes (fp8_attention.py:274-279).
+
+    bits = s*8 + (56 - 8m) in fp32; code = 0 where bits < 8 or invalid, else
+    clamp(rint(bits), 0, 126).  Read as e4m3 the code is Mitchell's approximation
+    2**floor(x) * (1 + frac(x)) of 2**(s-m), with x rounded to 1/8.
+    """
+    cst = (F32(56.0) - F32(8.0) * m).astype(F32)
+    bits = (s * F32(8.0) + cst[..., None]).astype(F32)
+    clamped = np.minimum(np.maximum(np.rint(bits), F32(0.0)), F32(126.0))
+    code = np.where((bits < F32(8.0)) | ~valid, F32(0.0), clamped)
+    return code.astype(np.uint8)
+
+
+def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-1.0,
+             block_n=128):
+    """_fp8_attn_kernel (fp8_attention.py:215-297), fp32 result [B,H,Sq,D].
+
+    Per (b, h, Q tile I of 128 rows): m=-1e9, l=0, acc=acc_r=0 (236-239); KV tiles of
+    `block_n` keys are visited in the staggered order j = (j0 + i) % nk with
+    j0 = I*nk // nq (241-245).  Per tile: S = fp32(Q8 K8^T) * sQ * sK (253); invalid
+    entries (row >= Sq, key >= Sk, bias <= -1e8, mask False) get -1e9 after the bias
+    is added in the log2 domain (255-264); lazy max: m moves to the tile row max only
+    if it exceeds m + 8 or m is still -1e9, then acc, acc_r, l are scaled by
+    exp2(m_old - m_new) (266-272); P codes from p_codes (274-279); l += sum(P),
+    acc += P V (284-286); with repair_tau >= 0 the exact exp2(S - m) minus P is added
+    where P >= tau, through bf16 (288-292).  Epilogue: (acc + acc_r) * sV / max(l, 1e-12).
+    """
+    B, H, Sq, D = q8.shape
+    Sk = k8.shape[2]
+    nq = _cdiv(Sq, BLOCK_M)
+    nk = _cdiv(Sk, block_n)
+    do_repair = float(repair_tau) >= 0.0
+    tau = F32(repair_tau)
+    out = np.zeros((B, H, Sq, D), F32)
+    I = np.arange(nq)
+    j0 = (I * nk) // nq
+    rows = I[:, None] * BLOCK_M + np.arange(BLOCK_M)[None, :]
+    mask_m = rows < Sq                                              # [nq, 128]
+    for b in range(B):
+        kb_full = None if key_bias is None else np.asarray(key_bias, F32)[b]
+        km_full = None if key_mask is None else np.asarray(key_mask, bool)[b]
+        for h in range(H):
+            Qd = np.zeros((nq * BLOCK_M, D), np.float64)
+            Qd[:Sq] = e4m3_decode(q8[b, h])
+            Qd = Qd.reshape(nq, BLOCK_M, D)
+            Kd = np.zeros((nk * block_n, D), np.float64)
+            Kd[:Sk] = e4m3_decode(k8[b, h])
+            Vd = np.zeros((nk * block_n, D), np.float64)
+            Vd[:Sk] = e4m3_decode(v8t[b, h]).T
+            sqI = np.asarray(sq[b, h], F32)[:, None, None]                 # per-row scale (230-234)
+            m = np.full((nq, BLOCK_M), NEG, F32)
+            l = np.zeros((nq, BLOCK_M), F32)
+            acc = np.zeros((nq, BLOCK_M, D), F32)
+            acc_r = np.zeros((nq, BLOCK_M, D), F32)
+            for i in range(nk):
+                j = (j0 + i) % nk                                          # [nq]
+                cols = j[:, None] * block_n + np.arange(block_n)[None, :]  # [nq, BN]
+                mask_n = cols < Sk
+                Kt = Kd[cols]                                              # [nq, BN, D]
+                s = np.matmul(Qd, Kt.transpose(0, 2, 1)).astype(F32)
+                skj = np.asarray(sk[b, h], F32)[(j * block_n) // 128][:, None, None]
+                s = ((s * sqI).astype(F32) * skj).astype(F32)
+                valid = mask_m[:, :, None] & mask_n[:, None, :]
+                if kb_full is not None:
+                    kb = np.where(mask_n, kb_full[np.minimum(cols, Sk - 1)], F32(0.0)).astype(F32)
+                    valid = valid & (kb[:, None, :] > F32(-1.0e8))
+                    s = (s + (kb * F32(LOG2E)).astype(F32)[:, None, :]).astype(F32)
+                if km_full is not None:
+                    km = np.where(mask_n, km_full[np.minimum(cols, Sk - 1)], False)
+                    valid = valid & km[:, None, :]
+                s = np.where(valid, s, NEG).astype(F32)
+                rowmax = s.max(axis=2)
+                m_new = np.where((rowmax > (m + F32(8.0))) | (m == NEG), rowmax, m).astype(F32)
+                alpha = np.exp2((m - m_new).astype(F32)).astype(F32)
+                acc = (acc * alpha[..., None]).astype(F32)
+                acc_r = (acc_r * alpha[..., None]).astype(F32)
+                l = (l * alpha).astype(F32)
+                m = m_new
+                codes = p_codes(s, m, valid)
+                p = e4m3_decode(codes).astype(np.float64)
+                Vt = Vd[cols]                                              # [nq, BN, D]
+                l = (l + p.sum(axis=2)).astype(F32)
+                acc = (acc + np.matmul(p, Vt)).astype(F32)
+                if do_repair:
+                    p32 = p.astype(F32)
+                    p_exact = np.where(valid, np.exp2((s - m[..., None]).astype(F32)), F32(0.0)).astype(F32)
+                    delta = np.where(p32 >= tau, (p_exact - p32).astype(F32), F32(0.0)).astype(F32)
+                    acc_r = (acc_r + np.matmul(bf16_round(delta).astype(np.float64), Vt)).astype(F32)
+                    l = (l + delta.astype(np.float64).sum(axis=2)).astype(F32)
+            svd = np.asarray(sv[b, h], F32)[None, None, :]
+            o = (((acc + acc_r).astype(F32) * svd).astype(F32) /
+                 np.maximum(l, F32(1e-12))[..., None]).astype(F32)
+            out[b, h] = o.reshape(nq * BLOCK_M, D)[:Sq]
+    return out
+
+
+def fp8_attention(q, k, v, scale=None, key_mask=None, key_bias=None, repair_tau=-1.0,
+                  out_dtype="bf16", mu=None):
+    """fp8_attention (fp8_attention.py:300-403) on [B,H,S,D] arrays of input values.
+
+    Returns (out [B,H,Sq,D] rounded to bf16 (or fp16), intermediates dict).
+    ``mu`` replaces the key mean when given (the GPU reduction order is not fixed).
+    """
+    q = np.asarray(q, F32)
+    k = np.asarray(k, F32)
+    v = np.asarray(v, F32)
+    D = q.shape[-1]
+    c = (scale if scale is not None else 1.0 / math.sqrt(D)) * LOG2E
+    q8, sq = quantize_q(q, c)
+    if mu is None:
+        mu = key_mean(k)
+    k8, sk = quantize_k(k, mu)
+    v8t, sv = quantize_v(v)
+    o = attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau)
+    if out_dtype == "bf16":
+        o = bf16_round(o)
+    elif out_dtype == "fp16":
+        o = o.astype(np.float16).astype(F32)
+    return o, dict(q8=q8, sq=sq, k8=k8, sk=sk, v8t=v8t, sv=sv, mu=mu, c=F32(c))

@@ -1,0 +1,93 @@
+"""Oracle for the FP8 linear path (test infrastructure only).
+
+Restates kernels/fp8_linear.py of the reference:
+* ``quantize_rows``      <- _quantize_rows_kernel / quantize_rows  (fp8_linear.py:8-24, 27-42)
+* ``scaled_mm``          <- the torch._scaled_mm call             (fp8_linear.py:95-102)
+* ``lora_branch_add``    <- apply_lora_adapters                    (fp8_linear.py:45-55)
+* ``gelu_tanh``          <- the tanh-GELU that follows the MLP-up linear in the DiT FFN
+* ``fp8_linear_forward`` <- FP8Linear.forward                      (fp8_linear.py:87-108)
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .numerics import E4M3_MAX, bf16_round, e4m3_decode, e4m3_encode
+
+F32 = np.float32
+
+
+def quantize_rows(x):
+    """Per-row dynamic e4m3 quantization (fp8_linear.py:16-24).
+
+    x: [M, K] values (fp32 view of the bf16/fp16/fp32 input).
+    Returns (codes uint8 [M, K], scale fp32 [M, 1]):
+      scale = max(max_k |x|, 1e-12) / 448            (fp32, IEEE division, line 21)
+      code  = e4m3(clamp(x / scale, -448, 448))      (fp32 IEEE division, line 22)
+    """
+    x = np.asarray(x, dtype=F32)
+    if x.ndim != 2:
+        raise ValueError("quantize_rows expects a 2D array")
+    M, K = x.shape
+    if K == 0:
+        return np.zeros((M, 0), np.uint8), np.full((M, 1), F32(1e-12) / F32(E4M3_MAX), F32)
+    amax = np.max(np.abs(x), axis=1)
+    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    q = (x / scale[:, None]).astype(F32)
+    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
+    return e4m3_encode(q), scale.reshape(M, 1)
+
+
+def scaled_mm(x8, w8, sa, sw, bias=None):
+    """Row-wise scaled FP8 GEMM, fp32-exact accumulate (fp8_linear.py:95-102).
+
+    out[m, n] = (sum_k dec(x8[m,k]) * dec(w8[n,k])) * sa[m] * sw[n] + bias[n]
+    x8 [M,K] codes, w8 [N,K] codes, sa [M] or [M,1], sw [N] or [1,N], bias [N] or None.
+    Returns fp32 [M, N] before the bf16 cast (products of e4m3 values are exact in
+    fp32; the sum is done in float64, the epilogue order of torch._scaled_mm is not
+    fixed by the reference).
+    """
+    a = e4m3_decode(x8).astype(np.float64)
+    b = e4m3_decode(w8).astype(np.float64)
+    acc = a @ b.T
+    out = acc * np.asarray(sa, np.float64).reshape(-1, 1) * np.asarray(sw, np.float64).reshape(1, -1)
+    if bias is not None:
+        out = out + np.asarray(bias, np.float64).reshape(1, -1)
+    return out.astype(F32)
+
+
+def gelu_tanh(z):
+    """0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3))), evaluated in float64."""
+    z = np.asarray(z, np.float64)
+    return (0.5 * z * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (z + 0.044715 * z ** 3)))).astype(F32)
+
+
+def lora_branch_add(x, out, adapters):
+    """apply_lora_adapters (fp8_linear.py:45-55) with torch's bf16 matmul rounding.
+
+    For each (A [r,K], B [N,r], scale): out = bf16(out + bf16(bf16(bf16(x@A^T) @ B^T) * scale)).
+    x, A, B are bf16-valued fp32 arrays; matmuls accumulate in float64 then round to bf16.
+    """
+    out = bf16_round(out)
+    x = bf16_round(x).astype(np.float64)
+    for A, B, scale in adapters:
+        t = bf16_round((x @ np.asarray(A, np.float64).T).astype(F32))
+        branch = bf16_round((t.astype(np.float64) @ np.asarray(B, np.float64).T).astype(F32))
+        branch = bf16_round((branch * F32(scale)).astype(F32))
+        out = bf16_round((out + branch).astype(F32))
+    return out
+
+
+def fp8_linear_forward(x, w8, w_scale, bias=None, adapters=(), gelu=False):
+    """FP8Linear.forward (fp8_linear.py:87-108) on [M, K] inputs, bf16 result as fp32.
+
+    Padding M to a multiple of 16 (lines 91-93) only adds zero rows whose outputs are
+    sliced away (line 106), so it does not change any kept value and is not modelled.
+    ``gelu`` applies the tanh-GELU of the following FFN activation after the LoRA add.
+    """
+    x = bf16_round(np.asarray(x, F32))
+    x8, sa = quantize_rows(x)
+    out = bf16_round(scaled_mm(x8, w8, sa, w_scale, bias))
+    out = lora_branch_add(x, out, adapters) if adapters else out
+    if gelu:
+        out = bf16_round(gelu_tanh(out))
+    return out

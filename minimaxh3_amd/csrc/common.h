@@ -1,0 +1,118 @@
+// Shared helpers for the MI355X (gfx950) FP8 hot-path kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mxf8.h"
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+namespace mxf8 {
+
+constexpr float kE4m3Max = 448.0f;
+constexpr float kScaleFloor = 1.0e-12f;
+
+// ---- error reporting (defined in capi.hip) --------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---- scalar conversions ---------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (inputs are finite on the hot path; NaN stays NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)f);
+}
+
+// Input element loaders: DT = MXF8_BF16 / MXF8_F16 / MXF8_F32.
+template <int DT> struct Elem;
+template <> struct Elem<MXF8_BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float to_f32(T v) { return bf16_bits_to_f32(v); }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+template <> struct Elem<MXF8_F16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float to_f32(T v) { return f16_bits_to_f32(v); }
+  static __device__ __forceinline__ float lo(uint32_t w) { return f16_bits_to_f32(w & 0xffffu); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return f16_bits_to_f32(w >> 16); }
+};
+template <> struct Elem<MXF8_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float to_f32(T v) { return v; }
+};
+
+// ---- quantisation arithmetic ----------------------------------------------------------
+// scale = max(amax, 1e-12) / 448 with IEEE division (the reference's fp32 semantics).
+__device__ __forceinline__ float e4m3_scale(float amax) {
+  return __fdiv_rn(fmaxf(amax, kScaleFloor), kE4m3Max);
+}
+
+// Correctly rounded x / s given r = RN(1/s): q0 = RN(x r) is faithful, the remainder
+// x - s q0 is exact with an fma, and RN(q0 + rem * r) is RN(x / s) (Markstein's
+// theorem, binary fp32, no overflow; quotients here are bounded by ~448).  The sign is
+// copied back because for x = -0 the remainder step yields +0 (IEEE -0 / s is -0).
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  float q0 = x * r;
+  float rem = __builtin_fmaf(-q0, s, x);
+  return __builtin_copysignf(__builtin_fmaf(rem, r, q0), x);
+}
+
+__device__ __forceinline__ float clamp448(float q) { return fminf(fmaxf(q, -kE4m3Max), kE4m3Max); }
+
+// Two fp32 values -> two e4m3fn bytes (RNE, hardware conversion) in the low 16 bits.
+__device__ __forceinline__ uint32_t cvt2_e4m3(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+// Four fp32 values -> four e4m3fn bytes packed little-endian in one dword.
+__device__ __forceinline__ uint32_t cvt4_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// ---- wave / block reductions ----------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Maximum over a 256-thread block; every thread gets the result.
+__device__ __forceinline__ float block256_max(float v, float* red4) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red4[w] = v;
+  __syncthreads();
+  float r = fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+  __syncthreads();
+  return r;
+}
+
+__host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace mxf8

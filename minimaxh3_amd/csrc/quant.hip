@@ -1,0 +1,521 @@
+// Dynamic e4m3 quantizers (HBM-bound): per-row activations/weights and the attention
+// Q / K / V quantizers.  One pass over the input wherever the statistic is local to
+// the tile (rows, 128-row blocks); the per-channel V scale and the key mean need a
+// reduction over the whole sequence first (a partial-reduction kernel writes one
+// [chunk][D] slab per workgroup into the caller's workspace and the consumer folds the
+// slabs in a fixed order, so results do not depend on scheduling).
+#include <stdarg.h>
+
+#include "common.h"
+
+namespace mxf8 {
+
+// ---------------------------------------------------------------------------------------
+// quantize_rows: kernels/fp8_linear.py:8-24 (per row: amax -> scale -> codes)
+// ---------------------------------------------------------------------------------------
+
+// Fast path: one wave per row, the whole row held in registers as NC 16-byte chunks per
+// lane (chunk c of lane l covers elements [(c*64 + l) * E, +E)).  Requires K % E == 0
+// and 16-byte aligned rows.
+template <int DT, int NC>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const void* __restrict__ x, int64_t M, int64_t K,
+                                                             int64_t ldx, uint8_t* __restrict__ x8,
+                                                             float* __restrict__ scale) {
+  typedef typename Elem<DT>::T T;
+  constexpr int E = 16 / sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const T*>(x) + row * ldx);
+  const int64_t nchunk = K / E;
+  uint4 v[NC];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    if (idx < nchunk) {
+      v[c] = xr[idx];
+    } else {
+      v[c] = make_uint4(0, 0, 0, 0);
+    }
+    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == MXF8_F32) {
+        amax = fmaxf(amax, fabsf(__uint_as_float(w[i])));
+      } else {
+        amax = fmaxf(amax, fmaxf(fabsf(Elem<DT>::lo(w[i])), fabsf(Elem<DT>::hi(w[i]))));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  const float s = e4m3_scale(amax);
+  const float r = __fdiv_rn(1.0f, s);
+  uint8_t* orow = x8 + row * K;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    if (idx < nchunk) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+      if constexpr (DT == MXF8_F32) {
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = clamp448(div_by_scale(__uint_as_float(w[i]), s, r));
+        *reinterpret_cast<uint32_t*>(orow + idx * 4) = cvt4_e4m3(f[0], f[1], f[2], f[3]);
+      } else {
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[2 * i] = clamp448(div_by_scale(Elem<DT>::lo(w[i]), s, r));
+          f[2 * i + 1] = clamp448(div_by_scale(Elem<DT>::hi(w[i]), s, r));
+        }
+        uint2 o;
+        o.x = cvt4_e4m3(f[0], f[1], f[2], f[3]);
+        o.y = cvt4_e4m3(f[4], f[5], f[6], f[7]);
+        *reinterpret_cast<uint2*>(orow + idx * 8) = o;
+      }
+    }
+  }
+  if (lane == 0) scale[row] = s;
+}
+
+// General path (any K, any alignment): one 256-thread block per row, two passes.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_rows_generic_kernel(const void* __restrict__ x, int64_t M,
+                                                                 int64_t K, int64_t ldx,
+                                                                 uint8_t* __restrict__ x8,
+                                                                 float* __restrict__ scale) {
+  typedef typename Elem<DT>::T T;
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = static_cast<const T*>(x) + row * ldx;
+  float amax = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(Elem<DT>::to_f32(xr[k])));
+  amax = block256_max(amax, red);
+  const float s = e4m3_scale(amax);
+  const float r = __fdiv_rn(1.0f, s);
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    const float q = clamp448(div_by_scale(Elem<DT>::to_f32(xr[k]), s, r));
+    x8[row * K + k] = (uint8_t)(cvt2_e4m3(q, 0.0f) & 0xff);
+  }
+  if (threadIdx.x == 0) scale[row] = s;
+}
+
+__global__ void fill_f32_kernel(float* p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+template <int DT, int NC>
+static void launch_quant_rows_reg(const void* x, int64_t M, int64_t K, int64_t ldx, uint8_t* x8, float* scale,
+                                  hipStream_t st) {
+  quant_rows_reg_kernel<DT, NC><<<dim3((unsigned)cdiv(M, 4)), dim3(256), 0, st>>>(x, M, K, ldx, x8, scale);
+}
+
+template <int DT>
+static int quant_rows_dispatch(const void* x, int64_t M, int64_t K, int64_t ldx, uint8_t* x8, float* scale,
+                               hipStream_t st) {
+  typedef typename Elem<DT>::T T;
+  constexpr int E = 16 / sizeof(T);
+  const bool aligned = (K % E == 0) && (ldx % E == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)x8 % 16 == 0);
+  const int64_t nchunk = K / E;
+  const int64_t per_lane = cdiv(nchunk, 64);
+  if (aligned && per_lane <= 32 && cdiv(M, 4) <= 0x7fffffff) {
+    switch (per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : per_lane <= 6 ? 6 : per_lane <= 8 ? 8
+            : per_lane <= 12 ? 12 : per_lane <= 16 ? 16 : per_lane <= 24 ? 24 : 32) {
+      case 1: launch_quant_rows_reg<DT, 1>(x, M, K, ldx, x8, scale, st); break;
+      case 2: launch_quant_rows_reg<DT, 2>(x, M, K, ldx, x8, scale, st); break;
+      case 4: launch_quant_rows_reg<DT, 4>(x, M, K, ldx, x8, scale, st); break;
+      case 6: launch_quant_rows_reg<DT, 6>(x, M, K, ldx, x8, scale, st); break;
+      case 8: launch_quant_rows_reg<DT, 8>(x, M, K, ldx, x8, scale, st); break;
+      case 12: launch_quant_rows_reg<DT, 12>(x, M, K, ldx, x8, scale, st); break;
+      case 16: launch_quant_rows_reg<DT, 16>(x, M, K, ldx, x8, scale, st); break;
+      case 24: launch_quant_rows_reg<DT, 24>(x, M, K, ldx, x8, scale, st); break;
+      default: launch_quant_rows_reg<DT, 32>(x, M, K, ldx, x8, scale, st); break;
+    }
+  } else {
+    if (M > 0x7fffffff) return set_error(MXF8_EINVAL, "quant_rows: M=%lld too large for the general path", (long long)M);
+    quant_rows_generic_kernel<DT><<<dim3((unsigned)M), dim3(256), 0, st>>>(x, M, K, ldx, x8, scale);
+  }
+  return check_launch("quant_rows");
+}
+
+// ---------------------------------------------------------------------------------------
+// Attention quantizers (kernels/fp8_attention.py:39-170)
+// ---------------------------------------------------------------------------------------
+
+struct Strides4 {
+  int64_t b, h, s, d;
+};
+
+// Loads 8 consecutive-in-d elements of row `s` as fp32.  VEC: d contiguous and the
+// 8-element group 16-byte aligned; otherwise element-wise strided loads.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(const void* base, const Strides4& st, int64_t s, int d0, float f[8]) {
+  typedef typename Elem<DT>::T T;
+  const T* p = static_cast<const T*>(base) + s * st.s + (int64_t)d0 * st.d;
+  if constexpr (VEC) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = Elem<DT>::lo(w[i]);
+      f[2 * i + 1] = Elem<DT>::hi(w[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = Elem<DT>::to_f32(p[(int64_t)i * st.d]);
+  }
+}
+
+// Q (IS_K = false) and K (IS_K = true) quantizer: one block per (128-row block, b*H + h).
+// Thread t handles the 8-wide d-chunk (t % CPR) of rows (t / CPR) + RPP * p.
+template <int DT, int D, bool IS_K, bool VEC>
+__global__ __launch_bounds__(256) void attn_quant_qk_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
+                                                            int64_t S, int64_t Sp, float c,
+                                                            const float* __restrict__ mean,
+                                                            uint8_t* __restrict__ out8,
+                                                            float* __restrict__ scale_out) {
+  constexpr int CPR = D / 8;      // chunks per row
+  constexpr int RPP = 256 / CPR;  // rows per pass
+  constexpr int NP = 128 / RPP;   // passes
+  __shared__ float red[4];
+  const int64_t blk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / H, h = bh % H;
+  const void* base = static_cast<const char*>(src) + (b * st.b + h * st.h) * (int64_t)sizeof(typename Elem<DT>::T);
+  const int cc = threadIdx.x % CPR;
+  const int rl = threadIdx.x / CPR;
+  float mu[8];
+  if constexpr (IS_K) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mu[i] = mean[bh * D + cc * 8 + i];
+  }
+  float f[NP][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t s = blk * 128 + rl + RPP * p;
+    if (s < S) {
+      load8<DT, VEC>(base, st, s, cc * 8, f[p]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        f[p][i] = IS_K ? (f[p][i] - mu[i]) : (f[p][i] * c);
+        amax = fmaxf(amax, fabsf(f[p][i]));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[p][i] = 0.0f;
+    }
+  }
+  amax = block256_max(amax, red);
+  const float sc = e4m3_scale(amax);
+  const float r = __fdiv_rn(1.0f, sc);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int64_t s = blk * 128 + rl + RPP * p;  // rows in [S, Sp) are written as zeros
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = clamp448(div_by_scale(f[p][i], sc, r));
+    uint2 o;
+    o.x = cvt4_e4m3(q[0], q[1], q[2], q[3]);
+    o.y = cvt4_e4m3(q[4], q[5], q[6], q[7]);
+    *reinterpret_cast<uint2*>(out8 + (bh * Sp + s) * D + cc * 8) = o;
+  }
+  if (threadIdx.x == 0) scale_out[bh * gridDim.x + blk] = sc;
+}
+
+// Partial column reductions over a chunk of rows: SUM (key mean) or ABSMAX (V scale).
+// grid (nch, B*H); writes part[bh][chunk][d].
+template <int DT, int D, bool ABSMAX, bool VEC>
+__global__ __launch_bounds__(256) void attn_colreduce_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
+                                                             int64_t S, int64_t rows_per_chunk,
+                                                             float* __restrict__ part) {
+  constexpr int CPR = D / 8;
+  constexpr int RPP = 256 / CPR;
+  __shared__ float red[RPP][D + 1];
+  const int64_t ch = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / H, h = bh % H;
+  const void* base = static_cast<const char*>(src) + (b * st.b + h * st.h) * (int64_t)sizeof(typename Elem<DT>::T);
+  const int cc = threadIdx.x % CPR;
+  const int rl = threadIdx.x / CPR;
+  const int64_t r0 = ch * rows_per_chunk;
+  const int64_t r1 = min(S, r0 + rows_per_chunk);
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int64_t s = r0 + rl; s < r1; s += RPP) {
+    float f[8];
+    load8<DT, VEC>(base, st, s, cc * 8, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = ABSMAX ? fmaxf(acc[i], fabsf(f[i])) : acc[i] + f[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[rl][cc * 8 + i] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float a = red[0][threadIdx.x];
+    for (int j = 1; j < RPP; ++j) a = ABSMAX ? fmaxf(a, red[j][threadIdx.x]) : a + red[j][threadIdx.x];
+    part[(bh * gridDim.x + ch) * D + threadIdx.x] = a;
+  }
+}
+
+// mean[bh][d] = (sum over chunks, in order) / S
+template <int D>
+__global__ void attn_kmean_finalize_kernel(const float* __restrict__ part, int nch, int64_t S,
+                                           float* __restrict__ mean) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  if (d >= D) return;
+  float a = 0.0f;
+  for (int c = 0; c < nch; ++c) a += part[(bh * nch + c) * D + d];
+  mean[bh * D + d] = __fdiv_rn(a, (float)S);
+}
+
+// V quantizer, transposed store.  grid (Skp/128, B*H).  Each block folds the per-chunk
+// absmax slabs into sv (fixed order; max is exact), quantizes a 128-key x D tile and
+// writes it transposed through LDS so that every v8t row segment is a full 128 bytes.
+// Thread t handles d-chunk (t % CPR) of the 4 consecutive keys 4 * (t / CPR + KQP * p) + 0..3.
+template <int DT, int D, bool VEC>
+__global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
+                                                           int64_t S, int64_t Sp, const float* __restrict__ part,
+                                                           int nch, uint8_t* __restrict__ v8t,
+                                                           float* __restrict__ sv) {
+  constexpr int CPR = D / 8;
+  constexpr int KQP = 256 / CPR;  // key quads per pass
+  constexpr int NP = 32 / KQP;    // passes over the 32 key quads of the tile
+  constexpr int LDS_STRIDE = 128 + 4;
+  __shared__ uint8_t tile[D * LDS_STRIDE];
+  __shared__ float s_sv[D];
+  __shared__ float s_r[D];
+  const int64_t blk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / H, h = bh % H;
+  if (threadIdx.x < D) {
+    float a = 0.0f;
+    for (int c = 0; c < nch; ++c) a = fmaxf(a, part[(bh * nch + c) * D + threadIdx.x]);
+    const float s = e4m3_scale(a);
+    s_sv[threadIdx.x] = s;
+    s_r[threadIdx.x] = __fdiv_rn(1.0f, s);
+    if (blk == 0) sv[bh * D + threadIdx.x] = s;
+  }
+  __syncthreads();
+  const void* base = static_cast<const char*>(src) + (b * st.b + h * st.h) * (int64_t)sizeof(typename Elem<DT>::T);
+  const int cc = threadIdx.x % CPR;
+  float scl[8], rcp[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    scl[i] = s_sv[cc * 8 + i];
+    rcp[i] = s_r[cc * 8 + i];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int kq = threadIdx.x / CPR + KQP * p;
+    uint32_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // col[i]: 4 key bytes of channel cc*8+i
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t s = blk * 128 + kq * 4 + j;
+      float f[8];
+      if (s < S) {
+        load8<DT, VEC>(base, st, s, cc * 8, f);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint32_t two = cvt2_e4m3(clamp448(div_by_scale(f[i], scl[i], rcp[i])),
+                                       clamp448(div_by_scale(f[i + 1], scl[i + 1], rcp[i + 1])));
+        col[i] |= (two & 0xffu) << (8 * j);
+        col[i + 1] |= (two >> 8) << (8 * j);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint32_t*>(&tile[(cc * 8 + i) * LDS_STRIDE + kq * 4]) = col[i];
+  }
+  __syncthreads();
+  // D rows x 128 bytes, 16 bytes per thread-step
+  constexpr int CHUNKS = D * 8;
+  for (int x = threadIdx.x; x < CHUNKS; x += 256) {
+    const int d = x >> 3, kc = x & 7;
+    const uint32_t* src4 = reinterpret_cast<const uint32_t*>(&tile[d * LDS_STRIDE + kc * 16]);
+    uint4 o = make_uint4(src4[0], src4[1], src4[2], src4[3]);
+    *reinterpret_cast<uint4*>(v8t + (bh * D + d) * Sp + blk * 128 + kc * 16) = o;
+  }
+}
+
+static bool attn_vec_ok(const void* p, int dtype, const Strides4& st) {
+  const int64_t es = dtype == MXF8_F32 ? 4 : 2;
+  return st.d == 1 && ((uintptr_t)p % 16 == 0) && ((st.b * es) % 16 == 0) && ((st.h * es) % 16 == 0) &&
+         ((st.s * es) % 16 == 0);
+}
+
+static int attn_common_checks(const char* what, const void* src, int dtype, int64_t B, int64_t H, int64_t S,
+                              int64_t D) {
+  if (!src) return set_error(MXF8_EINVAL, "%s: null input", what);
+  if (dtype != MXF8_BF16 && dtype != MXF8_F16)
+    return set_error(MXF8_EINVAL, "%s: dtype must be bf16 or fp16", what);
+  if (D != 64 && D != 128) return set_error(MXF8_EINVAL, "%s: D must be 64 or 128 (got %lld)", what, (long long)D);
+  if (B <= 0 || H <= 0 || S <= 0) return set_error(MXF8_EINVAL, "%s: empty shape", what);
+  if (B * H > 65535) return set_error(MXF8_EINVAL, "%s: B*H must be <= 65535", what);
+  return MXF8_OK;
+}
+
+// Number of row chunks for the column reductions: enough blocks to fill the chip.
+static int colreduce_chunks(int64_t BH, int64_t S) {
+  int64_t nch = cdiv(2048, BH);
+  nch = nch < 1 ? 1 : nch;
+  nch = nch > 64 ? 64 : nch;
+  const int64_t max_by_rows = cdiv(S, 64);
+  return (int)(nch < max_by_rows ? nch : max_by_rows);
+}
+
+}  // namespace mxf8
+
+using namespace mxf8;
+
+extern "C" int mxf8_quant_rows(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* x8,
+                               float* scale, hipStream_t stream) {
+  if (M < 0 || K < 0) return set_error(MXF8_EINVAL, "quant_rows: negative shape");
+  if (M == 0) return MXF8_OK;
+  if (!scale) return set_error(MXF8_EINVAL, "quant_rows: null scale");
+  if (K == 0) {
+    fill_f32_kernel<<<dim3((unsigned)cdiv(M, 256)), dim3(256), 0, stream>>>(scale, M, kScaleFloor / kE4m3Max);
+    return check_launch("quant_rows(fill)");
+  }
+  if (!x || !x8) return set_error(MXF8_EINVAL, "quant_rows: null pointer");
+  if (ldx < K) return set_error(MXF8_EINVAL, "quant_rows: ldx < K");
+  switch (dtype) {
+    case MXF8_BF16: return quant_rows_dispatch<MXF8_BF16>(x, M, K, ldx, x8, scale, stream);
+    case MXF8_F16: return quant_rows_dispatch<MXF8_F16>(x, M, K, ldx, x8, scale, stream);
+    case MXF8_F32: return quant_rows_dispatch<MXF8_F32>(x, M, K, ldx, x8, scale, stream);
+    default: return set_error(MXF8_EINVAL, "quant_rows: unknown dtype %d", dtype);
+  }
+}
+
+extern "C" int64_t mxf8_attn_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
+  (void)Sq;
+  if (B <= 0 || H <= 0 || Sk <= 0 || D <= 0) return 0;
+  return (int64_t)colreduce_chunks(B * H, Sk) * B * H * D * (int64_t)sizeof(float);
+}
+
+template <int DT, int D, bool IS_K>
+static void launch_qk(const void* src, const Strides4& st, bool vec, int64_t H, int64_t S, int64_t BH, float c,
+                      const float* mean, uint8_t* out8, float* sc, hipStream_t stream) {
+  const int64_t nb = cdiv(S, 128);
+  dim3 grid((unsigned)nb, (unsigned)BH);
+  if (vec)
+    attn_quant_qk_kernel<DT, D, IS_K, true><<<grid, 256, 0, stream>>>(src, st, H, S, nb * 128, c, mean, out8, sc);
+  else
+    attn_quant_qk_kernel<DT, D, IS_K, false><<<grid, 256, 0, stream>>>(src, st, H, S, nb * 128, c, mean, out8, sc);
+}
+
+template <bool IS_K>
+static int quant_qk(const char* what, const void* src, int dtype, const int64_t strides[4], const float* mean,
+                    int64_t B, int64_t H, int64_t S, int64_t D, float c, uint8_t* out8, float* sc,
+                    hipStream_t stream) {
+  int rc = attn_common_checks(what, src, dtype, B, H, S, D);
+  if (rc) return rc;
+  if (!strides || !out8 || !sc || (IS_K && !mean)) return set_error(MXF8_EINVAL, "%s: null pointer", what);
+  if (cdiv(S, 128) > 0x7fffffff) return set_error(MXF8_EINVAL, "%s: S too large", what);
+  const Strides4 st{strides[0], strides[1], strides[2], strides[3]};
+  const bool vec = attn_vec_ok(src, dtype, st);
+  const int64_t BH = B * H;
+  if (dtype == MXF8_BF16) {
+    if (D == 128) launch_qk<MXF8_BF16, 128, IS_K>(src, st, vec, H, S, BH, c, mean, out8, sc, stream);
+    else launch_qk<MXF8_BF16, 64, IS_K>(src, st, vec, H, S, BH, c, mean, out8, sc, stream);
+  } else {
+    if (D == 128) launch_qk<MXF8_F16, 128, IS_K>(src, st, vec, H, S, BH, c, mean, out8, sc, stream);
+    else launch_qk<MXF8_F16, 64, IS_K>(src, st, vec, H, S, BH, c, mean, out8, sc, stream);
+  }
+  return check_launch(what);
+}
+
+extern "C" int mxf8_attn_quant_q(const void* q, int dtype, const int64_t strides[4], int64_t B, int64_t H,
+                                 int64_t S, int64_t D, float c, uint8_t* q8, float* sq, hipStream_t stream) {
+  return quant_qk<false>("attn_quant_q", q, dtype, strides, nullptr, B, H, S, D, c, q8, sq, stream);
+}
+
+extern "C" int mxf8_attn_quant_k(const void* k, int dtype, const int64_t strides[4], const float* mean,
+                                 int64_t B, int64_t H, int64_t S, int64_t D, uint8_t* k8, float* sk,
+                                 hipStream_t stream) {
+  return quant_qk<true>("attn_quant_k", k, dtype, strides, mean, B, H, S, D, 0.0f, k8, sk, stream);
+}
+
+template <int DT, int D, bool ABSMAX>
+static void launch_colreduce(const void* src, const Strides4& st, bool vec, int64_t H, int64_t S, int64_t BH,
+                             int nch, float* part, hipStream_t stream) {
+  const int64_t rpc = cdiv(S, nch);
+  dim3 grid((unsigned)nch, (unsigned)BH);
+  if (vec)
+    attn_colreduce_kernel<DT, D, ABSMAX, true><<<grid, 256, 0, stream>>>(src, st, H, S, rpc, part);
+  else
+    attn_colreduce_kernel<DT, D, ABSMAX, false><<<grid, 256, 0, stream>>>(src, st, H, S, rpc, part);
+}
+
+template <bool ABSMAX>
+static void colreduce(const void* src, int dtype, const Strides4& st, bool vec, int64_t H, int64_t S, int64_t D,
+                      int64_t BH, int nch, float* part, hipStream_t stream) {
+  if (dtype == MXF8_BF16) {
+    if (D == 128) launch_colreduce<MXF8_BF16, 128, ABSMAX>(src, st, vec, H, S, BH, nch, part, stream);
+    else launch_colreduce<MXF8_BF16, 64, ABSMAX>(src, st, vec, H, S, BH, nch, part, stream);
+  } else {
+    if (D == 128) launch_colreduce<MXF8_F16, 128, ABSMAX>(src, st, vec, H, S, BH, nch, part, stream);
+    else launch_colreduce<MXF8_F16, 64, ABSMAX>(src, st, vec, H, S, BH, nch, part, stream);
+  }
+}
+
+extern "C" int mxf8_attn_kmean(const void* k, int dtype, const int64_t strides[4], int64_t B, int64_t H,
+                               int64_t S, int64_t D, float* mean, void* workspace, hipStream_t stream) {
+  int rc = attn_common_checks("attn_kmean", k, dtype, B, H, S, D);
+  if (rc) return rc;
+  if (!strides || !mean || !workspace) return set_error(MXF8_EINVAL, "attn_kmean: null pointer");
+  const Strides4 st{strides[0], strides[1], strides[2], strides[3]};
+  const int64_t BH = B * H;
+  const int nch = colreduce_chunks(BH, S);
+  float* part = static_cast<float*>(workspace);
+  colreduce<false>(k, dtype, st, attn_vec_ok(k, dtype, st), H, S, D, BH, nch, part, stream);
+  rc = check_launch("attn_kmean(partial)");
+  if (rc) return rc;
+  if (D == 128)
+    attn_kmean_finalize_kernel<128><<<dim3((unsigned)BH), dim3(128), 0, stream>>>(part, nch, S, mean);
+  else
+    attn_kmean_finalize_kernel<64><<<dim3((unsigned)BH), dim3(64), 0, stream>>>(part, nch, S, mean);
+  return check_launch("attn_kmean(finalize)");
+}
+
+template <int DT, int D>
+static void launch_quant_v(const void* v, const Strides4& st, bool vec, int64_t H, int64_t S, int64_t BH,
+                           const float* part, int nch, uint8_t* v8t, float* sv, hipStream_t stream) {
+  const int64_t nb = cdiv(S, 128);
+  dim3 grid((unsigned)nb, (unsigned)BH);
+  if (vec)
+    attn_quant_v_kernel<DT, D, true><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, part, nch, v8t, sv);
+  else
+    attn_quant_v_kernel<DT, D, false><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, part, nch, v8t, sv);
+}
+
+extern "C" int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides[4], int64_t B, int64_t H,
+                                 int64_t S, int64_t D, uint8_t* v8t, float* sv, void* workspace,
+                                 hipStream_t stream) {
+  int rc = attn_common_checks("attn_quant_v", v, dtype, B, H, S, D);
+  if (rc) return rc;
+  if (!strides || !v8t || !sv || !workspace) return set_error(MXF8_EINVAL, "attn_quant_v: null pointer");
+  const Strides4 st{strides[0], strides[1], strides[2], strides[3]};
+  const bool vec = attn_vec_ok(v, dtype, st);
+  const int64_t BH = B * H;
+  const int nch = colreduce_chunks(BH, S);
+  float* part = static_cast<float*>(workspace);
+  colreduce<true>(v, dtype, st, vec, H, S, D, BH, nch, part, stream);
+  rc = check_launch("attn_quant_v(absmax)");
+  if (rc) return rc;
+  if (dtype == MXF8_BF16) {
+    if (D == 128) launch_quant_v<MXF8_BF16, 128>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+    else launch_quant_v<MXF8_BF16, 64>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+  } else {
+    if (D == 128) launch_quant_v<MXF8_F16, 128>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+    else launch_quant_v<MXF8_F16, 64>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+  }
+  return check_launch("attn_quant_v");
+}

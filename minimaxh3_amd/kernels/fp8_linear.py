@@ -1,0 +1,200 @@
+"""Drop-in FP8 linear path (mirrors kernels/fp8_linear.py of the reference).
+
+Same public surface: ``quantize_rows``, ``apply_lora_adapters``, ``FP8Linear`` (buffers
+``w8``, ``w_scale``, ``bias``; attributes ``in_features``, ``out_features``, ``adapters``),
+``find_primary_block_list`` and ``convert_transformer_to_fp8``.  The compute runs in the
+gfx950 HIP kernels of ``minimaxh3_amd`` (per-row e4m3 quantizer, row-wise scaled FP8 GEMM
+with the bias / LoRA / GELU-tanh epilogue fused); there is no fallback path.
+
+Differences from the reference that do not change results: no padding of M to a
+multiple of 16 (fp8_linear.py:91-93; the GEMM handles any M), and the LoRA branch of
+FP8Linear runs inside the GEMM epilogue instead of as separate bf16 matmuls + add.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from .. import ops
+
+ACT_NONE = 0
+ACT_GELU_TANH = 1
+
+
+def quantize_rows(x2d: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row dynamic e4m3 quantization (fp8_linear.py:27-42).
+
+    Returns (x8 [M, K] float8_e4m3fn, x_scale [M, 1] fp32) with
+    x_scale = max(max|row|, 1e-12) / 448 and x8 = e4m3(clamp(x / x_scale, +-448)).
+    """
+    if x2d.ndim != 2 or not x2d.is_cuda:
+        raise ValueError("quantize_rows expects a 2D CUDA tensor")
+    return ops.quant_rows(x2d)
+
+
+def apply_lora_adapters(
+    x: torch.Tensor,
+    out: torch.Tensor,
+    adapters: list[tuple[torch.Tensor, torch.Tensor, float]],
+) -> torch.Tensor:
+    """out + bf16(bf16(bf16(x A^T) B^T) * scale) for each adapter (fp8_linear.py:45-55).
+
+    This generic form serves the bf16 ``nn.Linear`` modules that the LoRA registry wraps
+    (runtime/lora.py:206-226); ``FP8Linear`` fuses the same branch into its GEMM.
+    """
+    if not adapters:
+        return out
+    for A, B, scale in adapters:
+        branch = (x.to(A.dtype) @ A.t()) @ B.t()
+        out = out + (branch * scale).to(out.dtype)
+    return out
+
+
+class FP8Linear(nn.Module):
+    """nn.Linear replacement with e4m3 weights and per-output-channel scales (fp8_linear.py:58-108)."""
+
+    def __init__(self, in_features: int, out_features: int) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.adapters: list[tuple[torch.Tensor, torch.Tensor, float]] = []
+        self.act = ACT_NONE
+        self._lora_cache_key = None
+        self._lora_cache = None
+
+    @classmethod
+    @torch.no_grad()
+    def from_linear(cls, linear: nn.Linear) -> "FP8Linear":
+        """Quantize ``linear``'s weight per output channel and free it (fp8_linear.py:65-85)."""
+        mod = cls(linear.in_features, linear.out_features)
+        weight = linear.weight.detach()
+        if not weight.is_cuda:
+            weight = weight.cuda()
+        w8, w_scale_col = quantize_rows(weight)
+        mod.register_buffer("w8", w8)
+        mod.register_buffer("w_scale", w_scale_col.view(1, -1).contiguous())
+        bias = None
+        if linear.bias is not None:
+            bias = linear.bias.detach().to(device=w8.device, dtype=torch.bfloat16).contiguous()
+        mod.register_buffer("bias", bias)
+        if isinstance(getattr(linear, "adapters", None), list):
+            mod.adapters = list(linear.adapters)
+        linear.weight = None
+        linear.bias = None
+        return mod
+
+    def _lora_operands(self, x2d: torch.Tensor):
+        """(t = bf16(x A^T), B, scale) for the fused epilogue, or (None, None, 0.0).
+
+        One adapter is applied with exactly the reference's roundings.  Several adapters
+        are concatenated along the rank with each scale folded into its B (bf16), which
+        rounds the branch sum once instead of once per adapter.  Ranks are zero-padded to
+        a multiple of 16 (the bf16 MFMA K step); the zero columns add nothing.
+        """
+        adapters = self.adapters
+        if not adapters:
+            return None, None, 0.0
+        key = tuple((id(A), id(B), float(s)) for A, B, s in adapters)
+        if key != self._lora_cache_key:
+            if len(adapters) == 1:
+                A, B, scale = adapters[0]
+                a, b = self._pad_rank(A.to(torch.bfloat16), B.to(torch.bfloat16))
+            else:
+                a = torch.cat([A.to(torch.bfloat16) for A, _, _ in adapters], 0)
+                b = torch.cat([(B.float() * float(s)).to(torch.bfloat16) for _, B, s in adapters], 1)
+                a, b = self._pad_rank(a, b)
+                scale = 1.0
+            self._lora_cache = (a.contiguous(), b.contiguous(), float(scale))
+            self._lora_cache_key = key
+        a, b, scale = self._lora_cache
+        xb = x2d if x2d.dtype == torch.bfloat16 else x2d.to(torch.bfloat16)
+        return ops.lora_down(xb, a), b, scale
+
+    @staticmethod
+    def _pad_rank(A: torch.Tensor, B: torch.Tensor):
+        r = A.shape[0]
+        rp = -(-r // 16) * 16
+        if rp != r:
+            A = torch.cat([A, A.new_zeros((rp - r, A.shape[1]))], 0)
+            B = torch.cat([B, B.new_zeros((B.shape[0], rp - r))], 1)
+        return A, B
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        orig_shape = x.shape
+        x2d = x.reshape(-1, self.in_features)
+        x8, x_scale = quantize_rows(x2d)
+        lora_t, lora_b, lora_scale = self._lora_operands(x2d)
+        out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
+                               lora_scale)
+        return out.reshape(*orig_shape[:-1], self.out_features).to(x.dtype)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, act={self.act}"
+
+
+def find_primary_block_list(transformer: nn.Module) -> tuple[str, nn.ModuleList]:
+    """The longest non-empty ModuleList, preferring lists of one module type (fp8_linear.py:111-122)."""
+    lists = [(n, m) for n, m in transformer.named_modules() if isinstance(m, nn.ModuleList) and len(m) > 0]
+    if not lists:
+        raise ValueError("No non-empty nn.ModuleList found in transformer")
+    uniform = [(n, m) for n, m in lists if len({type(c) for c in m}) == 1]
+    pool = uniform or lists
+    return max(pool, key=lambda nm: len(nm[1]))
+
+
+def _fuse_gelu_modules(block: nn.Module) -> None:
+    """Fold a tanh-GELU activation module into its FP8 projection (GEMM epilogue).
+
+    Matches the activation modules of diffusers-style FFNs: a module with a ``proj``
+    sub-module and ``approximate == "tanh"`` whose forward is gelu_tanh(proj(x)).
+    """
+    for name, mod in list(block.named_modules()):
+        proj = getattr(mod, "proj", None)
+        if isinstance(proj, FP8Linear) and getattr(mod, "approximate", None) == "tanh" and proj.act == ACT_NONE:
+            proj.act = ACT_GELU_TANH
+            mod.forward = proj.forward  # the module's own forward would apply GELU a second time
+
+
+def convert_transformer_to_fp8(
+    transformer: nn.Module,
+    exclude_patterns: str | list[str],
+    keep_edge_blocks: int,
+    fuse_gelu: bool = False,
+) -> int:
+    """Swap eligible nn.Linear modules of the primary blocks for FP8Linear (fp8_linear.py:125-162).
+
+    Blocks [keep, n - keep) are converted; a Linear qualifies when in/out features are
+    multiples of 16 and its lower-cased path contains none of the exclude patterns.
+    Returns the number of converted modules.  ``fuse_gelu`` additionally folds tanh-GELU
+    activations into the preceding FP8 GEMM (an extension; off by default).
+    """
+    if isinstance(exclude_patterns, str):
+        exclude_patterns = exclude_patterns.split(",")
+    patterns = [p.strip().lower() for p in exclude_patterns if p.strip()]
+    list_name, blocks = find_primary_block_list(transformer)
+    lo = max(0, int(keep_edge_blocks))
+    hi = max(lo, len(blocks) - int(keep_edge_blocks))
+    converted = 0
+    for idx in range(lo, hi):
+        block = blocks[idx]
+        for sub_name, sub in list(block.named_modules()):
+            if not isinstance(sub, nn.Linear):
+                continue
+            if sub.in_features % 16 or sub.out_features % 16:
+                continue
+            path = (f"{list_name}.{idx}.{sub_name}" if sub_name else f"{list_name}.{idx}").lower()
+            if any(p in path for p in patterns):
+                continue
+            new = FP8Linear.from_linear(sub)
+            if not sub_name:
+                blocks[idx] = new
+            else:
+                parent_name, _, attr = sub_name.rpartition(".")
+                parent = block.get_submodule(parent_name) if parent_name else block
+                setattr(parent, attr, new)
+            converted += 1
+        if fuse_gelu:
+            _fuse_gelu_modules(blocks[idx])
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+    return converted

@@ -1,0 +1,225 @@
+"""torch custom ops over libmxf8 (one per C-ABI entry point), with fake (meta) kernels.
+
+Registering the launches as ``torch.library.custom_op`` keeps the FP8 path opaque to
+torch.compile: the DiT blocks are compiled with ``fullgraph=False``
+(runtime/model_manager.py:127-141) and these ops trace as single nodes without graph
+breaks.  Outputs come from torch's caching allocator; launches go to the current stream.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as N
+
+E4M3 = torch.float8_e4m3fn
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _prep(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{what}: expected a GPU tensor")
+    N.require_gfx950(t.device)
+
+
+# ---------------------------------------------------------------------------------------
+# FP8 linear
+# ---------------------------------------------------------------------------------------
+
+@torch.library.custom_op("mxf8::quant_rows", mutates_args=())
+def quant_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """[M, K] bf16/fp16/fp32 -> (e4m3 [M, K], fp32 scale [M, 1]) (kernels/fp8_linear.py:27-42)."""
+    _prep(x, "quant_rows")
+    if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+        x = x.contiguous()
+    M, K = x.shape
+    x8 = torch.empty((M, K), dtype=E4M3, device=x.device)
+    scale = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    if M > 0:
+        with torch.cuda.device(x.device):
+            N.check(N.load().mxf8_quant_rows(x.data_ptr(), N.dtype_code(x.dtype), M, K, max(x.stride(0), K),
+                                             x8.data_ptr(), scale.data_ptr(), N.stream_of(x)), "quant_rows")
+    return x8, scale
+
+
+@quant_rows.register_fake
+def _(x):
+    M, K = x.shape
+    return x.new_empty((M, K), dtype=E4M3), x.new_empty((M, 1), dtype=torch.float32)
+
+
+@torch.library.custom_op("mxf8::gemm_rowwise", mutates_args=())
+def gemm_rowwise(a8: torch.Tensor, w8: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor,
+                 bias: torch.Tensor | None, act: int, lora_t: torch.Tensor | None,
+                 lora_b: torch.Tensor | None, lora_scale: float) -> torch.Tensor:
+    """bf16(a8 w8^T * sa * sw + bias) (+ LoRA) (+ GELU-tanh), bf16 [M, N]."""
+    _prep(a8, "gemm_rowwise")
+    M, K = a8.shape
+    Nn = w8.shape[0]
+    out = torch.empty((M, Nn), dtype=torch.bfloat16, device=a8.device)
+    if M == 0 or Nn == 0:
+        return out
+    r = 0 if lora_t is None else lora_t.shape[1]
+    with torch.cuda.device(a8.device):
+        N.check(N.load().mxf8_gemm_rowwise(
+            a8.data_ptr(), w8.data_ptr(), sa.data_ptr(), sw.data_ptr(), N.ptr(bias), int(act),
+            N.ptr(lora_t), N.ptr(lora_b), r, float(lora_scale), out.data_ptr(), M, Nn, K, Nn,
+            N.stream_of(a8)), "gemm_rowwise")
+    return out
+
+
+@gemm_rowwise.register_fake
+def _(a8, w8, sa, sw, bias, act, lora_t, lora_b, lora_scale):
+    return a8.new_empty((a8.shape[0], w8.shape[0]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("mxf8::lora_down", mutates_args=())
+def lora_down(x: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
+    """t = bf16(x A^T): x [M, K] bf16, A [r, K] bf16 -> [M, r] bf16 (kernels/fp8_linear.py:53)."""
+    _prep(x, "lora_down")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    a = a.contiguous()
+    M, K = x.shape
+    r = a.shape[0]
+    t = torch.empty((M, r), dtype=torch.bfloat16, device=x.device)
+    if M > 0:
+        with torch.cuda.device(x.device):
+            N.check(N.load().mxf8_lora_down(x.data_ptr(), x.stride(0), a.data_ptr(), t.data_ptr(), M, K, r,
+                                            N.stream_of(x)), "lora_down")
+    return t
+
+
+@lora_down.register_fake
+def _(x, a):
+    return x.new_empty((x.shape[0], a.shape[0]), dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------------------
+# FP8 attention
+# ---------------------------------------------------------------------------------------
+
+def _workspace(B: int, H: int, Sq: int, Sk: int, D: int, device) -> torch.Tensor:
+    n = int(N.load().mxf8_attn_workspace_bytes(B, H, Sq, Sk, D))
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
+@torch.library.custom_op("mxf8::attn_quant_q", mutates_args=())
+def attn_quant_q(q: torch.Tensor, c: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(q * c) -> Q8 [B,H,ceil(Sq/128)*128,D] e4m3 + sq [B,H,ceil(Sq/128)] (fp8_attention.py:39-77)."""
+    _prep(q, "attn_quant_q")
+    B, H, S, D = q.shape
+    nq = _cdiv(S, 128)
+    q8 = torch.empty((B, H, nq * 128, D), dtype=E4M3, device=q.device)
+    sq = torch.empty((B, H, nq), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        N.check(N.load().mxf8_attn_quant_q(q.data_ptr(), N.dtype_code(q.dtype), N.strides4(q), B, H, S, D,
+                                           float(c), q8.data_ptr(), sq.data_ptr(), N.stream_of(q)), "attn_quant_q")
+    return q8, sq
+
+
+@attn_quant_q.register_fake
+def _(q, c):
+    B, H, S, D = q.shape
+    nq = _cdiv(S, 128)
+    return q.new_empty((B, H, nq * 128, D), dtype=E4M3), q.new_empty((B, H, nq), dtype=torch.float32)
+
+
+@torch.library.custom_op("mxf8::attn_kmean", mutates_args=())
+def attn_kmean(k: torch.Tensor) -> torch.Tensor:
+    """Mean of fp32(k) over the key axis, [B, H, D] fp32 (fp8_attention.py:338)."""
+    _prep(k, "attn_kmean")
+    B, H, S, D = k.shape
+    mean = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
+    ws = _workspace(B, H, S, S, D, k.device)
+    with torch.cuda.device(k.device):
+        N.check(N.load().mxf8_attn_kmean(k.data_ptr(), N.dtype_code(k.dtype), N.strides4(k), B, H, S, D,
+                                         mean.data_ptr(), ws.data_ptr(), N.stream_of(k)), "attn_kmean")
+    return mean
+
+
+@attn_kmean.register_fake
+def _(k):
+    B, H, S, D = k.shape
+    return k.new_empty((B, H, D), dtype=torch.float32)
+
+
+@torch.library.custom_op("mxf8::attn_quant_k", mutates_args=())
+def attn_quant_k(k: torch.Tensor, mean: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(k - mean) -> K8 [B,H,ceil(Sk/128)*128,D] e4m3 + sk [B,H,ceil(Sk/128)] (fp8_attention.py:80-119)."""
+    _prep(k, "attn_quant_k")
+    B, H, S, D = k.shape
+    nk = _cdiv(S, 128)
+    mean = mean.to(torch.float32).contiguous()
+    k8 = torch.empty((B, H, nk * 128, D), dtype=E4M3, device=k.device)
+    sk = torch.empty((B, H, nk), dtype=torch.float32, device=k.device)
+    with torch.cuda.device(k.device):
+        N.check(N.load().mxf8_attn_quant_k(k.data_ptr(), N.dtype_code(k.dtype), N.strides4(k), mean.data_ptr(),
+                                           B, H, S, D, k8.data_ptr(), sk.data_ptr(), N.stream_of(k)), "attn_quant_k")
+    return k8, sk
+
+
+@attn_quant_k.register_fake
+def _(k, mean):
+    B, H, S, D = k.shape
+    nk = _cdiv(S, 128)
+    return k.new_empty((B, H, nk * 128, D), dtype=E4M3), k.new_empty((B, H, nk), dtype=torch.float32)
+
+
+@torch.library.custom_op("mxf8::attn_quant_v", mutates_args=())
+def attn_quant_v(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """v -> V8T [B,H,D,ceil(Sk/128)*128] e4m3 (transposed) + sv [B,H,D] (fp8_attention.py:122-170)."""
+    _prep(v, "attn_quant_v")
+    B, H, S, D = v.shape
+    nk = _cdiv(S, 128)
+    v8t = torch.empty((B, H, D, nk * 128), dtype=E4M3, device=v.device)
+    sv = torch.empty((B, H, D), dtype=torch.float32, device=v.device)
+    ws = _workspace(B, H, S, S, D, v.device)
+    with torch.cuda.device(v.device):
+        N.check(N.load().mxf8_attn_quant_v(v.data_ptr(), N.dtype_code(v.dtype), N.strides4(v), B, H, S, D,
+                                           v8t.data_ptr(), sv.data_ptr(), ws.data_ptr(), N.stream_of(v)),
+                "attn_quant_v")
+    return v8t, sv
+
+
+@attn_quant_v.register_fake
+def _(v):
+    B, H, S, D = v.shape
+    nk = _cdiv(S, 128)
+    return v.new_empty((B, H, D, nk * 128), dtype=E4M3), v.new_empty((B, H, D), dtype=torch.float32)
+
+
+@torch.library.custom_op("mxf8::attn_fwd", mutates_args=())
+def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Tensor, sk: torch.Tensor,
+             sv: torch.Tensor, key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, repair_tau: float,
+             like: torch.Tensor, Sk: int) -> torch.Tensor:
+    """FP8 flash-attention forward (fp8_attention.py:185-297).
+
+    ``like`` is the original query: the output has its shape, dtype and strides (the
+    kernel writes through the strides, so permuted query layouts stay correct).
+    """
+    _prep(q8, "attn_fwd")
+    B, H, Sq, D = like.shape
+    out = torch.empty_like(like)
+    km = None if key_mask is None else key_mask.to(torch.uint8).contiguous()
+    kb = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    with torch.cuda.device(q8.device):
+        N.check(N.load().mxf8_attn_fwd(
+            q8.data_ptr(), k8.data_ptr(), v8t.data_ptr(), sq.data_ptr(), sk.data_ptr(), sv.data_ptr(),
+            N.ptr(km), N.ptr(kb), float(repair_tau), out.data_ptr(), N.dtype_code(out.dtype), N.strides4(out),
+            B, H, Sq, Sk, D, N.stream_of(q8)), "attn_fwd")
+    return out
+
+
+@attn_fwd.register_fake
+def _(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, like, Sk):
+    return torch.empty_like(like)
+
+
+def softmax_c(scale: float | None, D: int) -> float:
+    """c = (scale or 1/sqrt(D)) * log2(e) (kernels/fp8_attention.py:315)."""
+    return (scale if scale is not None else 1.0 / math.sqrt(D)) * 1.4426950408889634

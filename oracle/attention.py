@@ -104,7 +104,7 @@ def p_codes(s, m, valid):
 
 
 def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-1.0,
-             block_n=128):
+             block_n=128, q_tiles=None):
     """_fp8_attn_kernel (fp8_attention.py:215-297), fp32 result [B,H,Sq,D].
 
     Per (b, h, Q tile I of 128 rows): m=-1e9, l=0, acc=acc_r=0 (236-239); KV tiles of
@@ -116,6 +116,8 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
     exp2(m_old - m_new) (266-272); P codes from p_codes (274-279); l += sum(P),
     acc += P V (284-286); with repair_tau >= 0 the exact exp2(S - m) minus P is added
     where P >= tau, through bf16 (288-292).  Epilogue: (acc + acc_r) * sV / max(l, 1e-12).
+    ``q_tiles`` restricts the work to those 128-row Q tiles (rows of other tiles stay 0);
+    tiles are independent, so this is exact for the rows it computes.
     """
     B, H, Sq, D = q8.shape
     Sk = k8.shape[2]
@@ -124,7 +126,8 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
     do_repair = float(repair_tau) >= 0.0
     tau = F32(repair_tau)
     out = np.zeros((B, H, Sq, D), F32)
-    I = np.arange(nq)
+    I = np.arange(nq) if q_tiles is None else np.asarray(q_tiles, np.int64)
+    ntile = len(I)
     j0 = (I * nk) // nq
     rows = I[:, None] * BLOCK_M + np.arange(BLOCK_M)[None, :]
     mask_m = rows < Sq                                              # [nq, 128]
@@ -134,16 +137,16 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
         for h in range(H):
             Qd = np.zeros((nq * BLOCK_M, D), np.float64)
             Qd[:Sq] = e4m3_decode(q8[b, h])
-            Qd = Qd.reshape(nq, BLOCK_M, D)
+            Qd = Qd.reshape(nq, BLOCK_M, D)[I]
             Kd = np.zeros((nk * block_n, D), np.float64)
             Kd[:Sk] = e4m3_decode(k8[b, h])
             Vd = np.zeros((nk * block_n, D), np.float64)
             Vd[:Sk] = e4m3_decode(v8t[b, h]).T
-            sqI = np.asarray(sq[b, h], F32)[:, None, None]                 # per-row scale (230-234)
-            m = np.full((nq, BLOCK_M), NEG, F32)
-            l = np.zeros((nq, BLOCK_M), F32)
-            acc = np.zeros((nq, BLOCK_M, D), F32)
-            acc_r = np.zeros((nq, BLOCK_M, D), F32)
+            sqI = np.asarray(sq[b, h], F32)[I][:, None, None]              # per-row scale (230-234)
+            m = np.full((ntile, BLOCK_M), NEG, F32)
+            l = np.zeros((ntile, BLOCK_M), F32)
+            acc = np.zeros((ntile, BLOCK_M, D), F32)
+            acc_r = np.zeros((ntile, BLOCK_M, D), F32)
             for i in range(nk):
                 j = (j0 + i) % nk                                          # [nq]
                 cols = j[:, None] * block_n + np.arange(block_n)[None, :]  # [nq, BN]
@@ -182,7 +185,10 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
             svd = np.asarray(sv[b, h], F32)[None, None, :]
             o = (((acc + acc_r).astype(F32) * svd).astype(F32) /
                  np.maximum(l, F32(1e-12))[..., None]).astype(F32)
-            out[b, h] = o.reshape(nq * BLOCK_M, D)[:Sq]
+            for n, tile in enumerate(I):
+                r0 = int(tile) * BLOCK_M
+                r1 = min(Sq, r0 + BLOCK_M)
+                out[b, h, r0:r1] = o[n, :r1 - r0]
     return out
 
 

@@ -1,0 +1,52 @@
+"""Shared helpers for the tests (not a test module)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle.numerics import bf16_round
+
+
+def bf16_randn(rng, shape, std=1.0):
+    """Seeded N(0, std^2) values rounded to bf16 (as fp32 numpy)."""
+    return bf16_round((rng.standard_normal(shape) * std).astype(np.float32))
+
+
+def with_outliers(rng, x, frac=0.01, factor=20.0):
+    """Scale a random `frac` of the last-axis channels by `factor` (activation outliers)."""
+    K = x.shape[-1]
+    idx = rng.choice(K, max(1, int(frac * K)), replace=False)
+    x = x.copy()
+    x[..., idx] *= factor
+    return bf16_round(x)
+
+
+def to_gpu(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device="cuda", dtype=dtype)
+
+
+def codes(t: torch.Tensor) -> np.ndarray:
+    """uint8 view of an e4m3 tensor as numpy."""
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def cos(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+
+
+def assert_gemm_close(out, ref, tol=1e-2):
+    """GEMM bar: max|out-ref| <= tol * max|ref| and ||out-ref|| / ||ref|| <= tol."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out - ref)
+    assert err.max() <= tol * np.abs(ref).max(), (err.max(), np.abs(ref).max())
+    assert np.linalg.norm(out - ref) <= tol * np.linalg.norm(ref)
+
+
+def assert_attn_close(out, ref, cos_min=0.999, max_abs=2e-2):
+    """Attention bar: cosine >= 0.999 and max-abs <= 2e-2 against the oracle."""
+    c = cos(out, ref)
+    m = float(np.max(np.abs(np.asarray(out, np.float64) - np.asarray(ref, np.float64))))
+    assert c >= cos_min and m <= max_abs, (c, m)

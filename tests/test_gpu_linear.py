@@ -1,0 +1,253 @@
+"""GPU parity of the FP8 linear path against the oracle (quantizer bit-exact, GEMM 1e-2)."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import linear as ol
+from oracle.numerics import bf16_round, e4m3_decode
+from tests.helpers import assert_gemm_close, bf16_randn, codes, to_gpu, with_outliers
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def fl():
+    from minimaxh3_amd.kernels import fp8_linear
+    return fp8_linear
+
+
+# ---------------------------------------------------------------- quantize_rows (a1/a2)
+
+@pytest.mark.parametrize("M,K,dtype", [
+    (37, 3072, torch.bfloat16), (16, 12288, torch.bfloat16), (5, 64, torch.bfloat16),
+    (33, 3072, torch.float16), (9, 1024, torch.float32), (7, 100, torch.bfloat16),
+    (3, 20000, torch.bfloat16), (1, 16, torch.float32),
+])
+def test_quantize_rows_bit_exact(fl, M, K, dtype):
+    _say(f"quantize_rows M={M} K={K} {dtype}")
+    rng = np.random.default_rng(M * 131 + K)
+    x = with_outliers(rng, bf16_randn(rng, (M, K)))
+    if dtype == torch.float16:
+        x = x.astype(np.float16).astype(np.float32)
+    if dtype == torch.float32:
+        x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    x8, sc = fl.quantize_rows(to_gpu(x, dtype))
+    torch.cuda.synchronize()
+    rc, rs = ol.quantize_rows(x)
+    assert x8.dtype == torch.float8_e4m3fn and x8.shape == (M, K)
+    assert sc.dtype == torch.float32 and sc.shape == (M, 1)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rs)
+    np.testing.assert_array_equal(codes(x8), rc)
+
+
+def test_quantize_rows_edge_cases(fl):
+    _say("quantize_rows edge cases")
+    x = np.zeros((6, 256), np.float32)
+    x[1, 3] = -3.0
+    x[1, 4] = 1.5
+    x[2] = -0.0
+    x[3, :] = 1e-30
+    # values that land exactly on e4m3 rounding midpoints after the division (ties)
+    x[4, 0] = 448.0
+    x[4, 1:9] = np.array([1.0625, 1.1875, 3.25, 0.0087890625, 2.125, 6.5, 13.0, 416.0]) * 1.0
+    x[5] = np.linspace(-7, 7, 256)
+    x = bf16_round(x)
+    x8, sc = fl.quantize_rows(to_gpu(x))
+    rc, rs = ol.quantize_rows(x)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rs)
+    np.testing.assert_array_equal(codes(x8), rc)
+    # empty and non-contiguous inputs
+    e8, es = fl.quantize_rows(torch.empty((0, 32), device="cuda", dtype=torch.bfloat16))
+    assert e8.shape == (0, 32) and es.shape == (0, 1)
+    big = to_gpu(bf16_randn(np.random.default_rng(1), (8, 512)))
+    view = big[:, 128:384]
+    v8, vs = fl.quantize_rows(view)
+    rc, rs = ol.quantize_rows(big[:, 128:384].float().cpu().numpy())
+    np.testing.assert_array_equal(codes(v8), rc)
+    with pytest.raises(ValueError):
+        fl.quantize_rows(torch.zeros(4, 4))            # CPU tensor
+    with pytest.raises(ValueError):
+        fl.quantize_rows(torch.zeros(4, 4, 4, device="cuda"))
+
+
+def test_quantize_rows_ties_at_every_midpoint(fl):
+    # Row amax 448 -> scale exactly 1: every e4m3 midpoint appears verbatim as x / s.
+    _say("quantize_rows midpoints")
+    c = np.arange(256, dtype=np.uint8)
+    vals = np.unique(e4m3_decode(c[(c & 0x7F) != 0x7F]).astype(np.float64))
+    mids = (vals[1:] + vals[:-1]) / 2
+    mids = mids[np.abs(mids) < 448]
+    row = np.concatenate([[448.0], mids]).astype(np.float32)
+    x = np.zeros((1, 512), np.float32)
+    x[0, :len(row)] = row
+    x8, sc = fl.quantize_rows(to_gpu(x, torch.float32))
+    rc, rs = ol.quantize_rows(x)
+    assert sc.item() == 1.0
+    np.testing.assert_array_equal(codes(x8), rc)
+
+
+# ---------------------------------------------------------------- scaled GEMM (a3/a4/a6)
+
+def _gemm_case(rng, M, N, K, bias=True):
+    x = with_outliers(rng, bf16_randn(rng, (M, K)))
+    w = bf16_randn(rng, (N, K), 0.02)
+    b = bf16_randn(rng, (N,), 0.01) if bias else None
+    x8, sa = ol.quantize_rows(x)
+    w8, sw = ol.quantize_rows(w)
+    return x, x8, sa, w8, sw, b
+
+
+@pytest.mark.parametrize("M,N,K,bias", [
+    (40, 96, 256, True), (300, 320, 400, True), (2048, 3072, 3072, True), (129, 64, 16, False),
+    (1, 3072, 3072, True), (600, 1040, 1152, False),
+])
+def test_gemm_rowwise_matches_oracle(M, N, K, bias):
+    _say(f"gemm M={M} N={N} K={K} bias={bias}")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(M + N + K)
+    x, x8, sa, w8, sw, b = _gemm_case(rng, M, N, K, bias)
+    out = ops.gemm_rowwise(to_gpu(x8, torch.uint8).view(torch.float8_e4m3fn),
+                           to_gpu(w8, torch.uint8).view(torch.float8_e4m3fn),
+                           to_gpu(sa, torch.float32), to_gpu(sw.reshape(1, -1), torch.float32),
+                           None if b is None else to_gpu(b), 0, None, None, 0.0)
+    ref = bf16_round(ol.scaled_mm(x8, w8, sa, sw, b))
+    assert out.dtype == torch.bfloat16 and out.shape == (M, N)
+    assert_gemm_close(out.float().cpu().numpy(), ref)
+
+
+def test_gemm_rowwise_gelu():
+    _say("gemm gelu")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(5)
+    M, N, K = 300, 512, 384
+    x, x8, sa, w8, sw, b = _gemm_case(rng, M, N, K)
+    out = ops.gemm_rowwise(to_gpu(x8, torch.uint8).view(torch.float8_e4m3fn),
+                           to_gpu(w8, torch.uint8).view(torch.float8_e4m3fn),
+                           to_gpu(sa, torch.float32), to_gpu(sw.reshape(1, -1), torch.float32), to_gpu(b), 1,
+                           None, None, 0.0)
+    ref = bf16_round(ol.gelu_tanh(bf16_round(ol.scaled_mm(x8, w8, sa, sw, b))))
+    assert_gemm_close(out.float().cpu().numpy(), ref)
+
+
+def test_gemm_rejects_bad_shapes():
+    from minimaxh3_amd import ops
+    from minimaxh3_amd._native import NativeError
+    a = torch.zeros((4, 24), device="cuda", dtype=torch.float8_e4m3fn)
+    w = torch.zeros((8, 24), device="cuda", dtype=torch.float8_e4m3fn)
+    s = torch.ones((4, 1), device="cuda")
+    with pytest.raises(NativeError):
+        ops.gemm_rowwise(a, w, s, torch.ones((1, 8), device="cuda"), None, 0, None, None, 0.0)
+
+
+# ---------------------------------------------------------------- FP8Linear module (a3, a5)
+
+def test_fp8linear_forward_matches_oracle(fl):
+    _say("FP8Linear forward")
+    rng = np.random.default_rng(7)
+    K, N = 512, 384
+    lin = torch.nn.Linear(K, N, bias=True).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(bf16_randn(rng, (N, K), 0.02)))
+        lin.bias.copy_(to_gpu(bf16_randn(rng, (N,), 0.01)))
+    w = lin.weight.detach().float().cpu().numpy()
+    b = lin.bias.detach().float().cpu().numpy()
+    mod = fl.FP8Linear.from_linear(lin)
+    assert lin.weight is None and mod.w8.dtype == torch.float8_e4m3fn and mod.w_scale.shape == (1, N)
+    w8, sw = ol.quantize_rows(w)
+    np.testing.assert_array_equal(codes(mod.w8), w8)
+    np.testing.assert_array_equal(mod.w_scale.cpu().numpy().ravel(), sw.ravel())
+    x = with_outliers(rng, bf16_randn(rng, (3, 77, K)))          # M = 231 (not a multiple of 16)
+    with torch.no_grad():
+        out = mod(to_gpu(x))
+    assert out.shape == (3, 77, N) and out.dtype == torch.bfloat16
+    ref = ol.fp8_linear_forward(x.reshape(-1, K), w8, sw, b).reshape(3, 77, N)
+    assert_gemm_close(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_fp8linear_lora_epilogue(fl, gelu):
+    _say(f"FP8Linear lora gelu={gelu}")
+    rng = np.random.default_rng(8)
+    M, K, N, r = 500, 768, 640, 64
+    lin = torch.nn.Linear(K, N, bias=True).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(bf16_randn(rng, (N, K), 0.02)))
+        lin.bias.copy_(to_gpu(bf16_randn(rng, (N,), 0.01)))
+    w, b = lin.weight.detach().float().cpu().numpy(), lin.bias.detach().float().cpu().numpy()
+    mod = fl.FP8Linear.from_linear(lin)
+    A = bf16_randn(rng, (r, K), 0.01 * 8)
+    B = bf16_randn(rng, (N, r), 0.01 * 8)
+    mod.adapters.append((to_gpu(A), to_gpu(B), 0.75))
+    mod.act = 1 if gelu else 0
+    x = with_outliers(rng, bf16_randn(rng, (M, K)))
+    out = mod(to_gpu(x)).float().cpu().numpy()
+    w8, sw = ol.quantize_rows(w)
+    ref = ol.fp8_linear_forward(x, w8, sw, b, adapters=[(A, B, 0.75)], gelu=gelu)
+    assert_gemm_close(out, ref)
+    # the LoRA delta must be visible at this tolerance (not silently dropped)
+    no_lora = ol.fp8_linear_forward(x, w8, sw, b, gelu=gelu)
+    assert np.abs(ref - no_lora).max() > 5e-2 * np.abs(ref).max()
+
+
+def test_fp8linear_two_adapters_odd_rank(fl):
+    _say("FP8Linear two adapters")
+    rng = np.random.default_rng(9)
+    M, K, N = 200, 256, 256
+    lin = torch.nn.Linear(K, N, bias=False).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(bf16_randn(rng, (N, K), 0.02)))
+    w = lin.weight.detach().float().cpu().numpy()
+    mod = fl.FP8Linear.from_linear(lin)
+    ads = []
+    for r, s in ((8, 1.0), (24, 0.5)):
+        A, B = bf16_randn(rng, (r, K), 0.1), bf16_randn(rng, (N, r), 0.1)
+        ads.append((A, B, s))
+        mod.adapters.append((to_gpu(A), to_gpu(B), s))
+    x = bf16_randn(rng, (M, K))
+    out = mod(to_gpu(x)).float().cpu().numpy()
+    w8, sw = ol.quantize_rows(w)
+    ref = ol.fp8_linear_forward(x, w8, sw, None, adapters=ads)
+    assert_gemm_close(out, ref)
+
+
+def test_lora_down_matches_bf16_matmul():
+    _say("lora_down")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(10)
+    for M, K, r in ((100, 3072, 64), (33, 520, 16), (257, 1024, 128), (64, 64, 48)):
+        x, A = bf16_randn(rng, (M, K)), bf16_randn(rng, (r, K), 0.05)
+        t = ops.lora_down(to_gpu(x), to_gpu(A)).float().cpu().numpy()
+        ref = bf16_round((x.astype(np.float64) @ A.astype(np.float64).T).astype(np.float32))
+        np.testing.assert_allclose(t, ref, rtol=2 ** -7, atol=1e-3 * np.abs(ref).max())
+
+
+# ---------------------------------------------------------------- full-size shapes (properties)
+
+@pytest.mark.parametrize("N,K", [(9216, 3072), (12288, 3072), (3072, 12288)])
+def test_dit_block_linear_shapes_sampled_rows(N, K):
+    """M = 20280 DiT-block linears: the whole output against the oracle on sampled rows."""
+    _say(f"DiT linear M=20280 N={N} K={K}")
+    from minimaxh3_amd import ops
+    M = 20280
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn((N, K), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn((N,), device="cuda", generator=g) * 0.01).to(torch.bfloat16)
+    x8, sa = ops.quant_rows(x)
+    w8, sw = ops.quant_rows(w)
+    out = ops.gemm_rowwise(x8, w8, sa, sw.view(1, -1), b, 0, None, None, 0.0)
+    torch.cuda.synchronize()
+    rows = np.r_[0:64, 10000:10064, M - 64:M]
+    xs = x[rows].float().cpu().numpy()
+    rc, rs = ol.quantize_rows(xs)
+    np.testing.assert_array_equal(codes(x8[rows]), rc)
+    ref = bf16_round(ol.scaled_mm(rc, codes(w8), rs, sw.cpu().numpy(), b.float().cpu().numpy()))
+    assert_gemm_close(out[rows].float().cpu().numpy(), ref)
+    assert torch.isfinite(out).all()

@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X FP8 hot path on one DiT block at 480p (one GPU).
+
+A step is one pass of the FP8 hot path over one DiT block's worth of synthetic inputs:
+
+* the four FP8 linears of the block at M = 20280 tokens (13 latent frames x 30 x 52
+  patches), hidden 3072: QKV 3072->9216, attention-out 3072->3072, MLP-up 3072->12288
+  with the fused GELU-tanh epilogue, MLP-down 12288->3072.  Each one is the FP8Linear
+  forward: per-token e4m3 activation quantization, then the row-wise scaled FP8 GEMM
+  with bias.  Activations bf16 ~N(0,1) with 1% of the channels scaled x20 (outliers),
+  weights ~N(0,0.02) quantized per output channel at load, bias ~N(0,0.01);
+* one non-causal FP8 flash-attention forward, B=1, H=24, S=20280, D=128: Q/K/V bf16
+  ~N(0,1) in the [B,S,H,D] storage of a fused QKV projection (permuted views), Q/K/V
+  quantizers, then the attention kernel; softmax scale 1/sqrt(128), repair off.
+
+value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
+4*B*H*Sq*Sk*D for the attention) / wall time of the step, in TFLOP/s, with every input
+resident in HBM before the timed region.  Each kernel of the step is also bracketed by
+HIP events on the stream it runs on; the attention kernel (the largest one) gives the
+roofline entry.  The CPU baseline times the reference's torch CPU fallbacks (fp32
+dequant-matmul and SDPA) on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "FP8 GEMM + FP8 attn TFLOP/s (S=20k, D=128) and % of MI355X FP8 peak, 1 GPU"
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+TOKENS = 20280                # 13 x 30 x 52
+HIDDEN, MLP = 3072, 12288
+HEADS, HEAD_DIM = 24, 128
+# (name, in_features, out_features, fused activation)
+LINEARS = (("qkv", HIDDEN, 3 * HIDDEN, 0), ("attn_out", HIDDEN, HIDDEN, 0),
+           ("mlp_up", HIDDEN, MLP, 1), ("mlp_down", MLP, HIDDEN, 0))
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemm_flops(m: int, n: int, k: int) -> float:
+    return 2.0 * m * n * k
+
+
+def attn_flops(b: int, h: int, sq: int, sk: int, d: int) -> float:
+    return 4.0 * b * h * sq * sk * d
+
+
+def activations(torch, g, m: int, k: int, dev):
+    """bf16 ~N(0,1) [m, k] with floor(1% of k) channels (seeded randperm) scaled x20."""
+    x = torch.randn((m, k), device=dev, generator=g)
+    idx = torch.randperm(k, device=dev, generator=g)[: k // 100]
+    x[:, idx] *= 20.0
+    return x.to(torch.bfloat16)
+
+
+def build_workload(torch, dev):
+    from minimaxh3_amd.kernels.fp8_linear import FP8Linear
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    linears = []
+    for name, k, n, act in LINEARS:
+        lin = torch.nn.Linear(k, n, bias=True, device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn((n, k), device=dev, generator=g) * 0.02)
+            lin.bias.copy_(torch.randn((n,), device=dev, generator=g) * 0.01)
+        mod = FP8Linear.from_linear(lin)
+        mod.act = act
+        linears.append((name, mod, activations(torch, g, TOKENS, k, dev)))
+    qkv = torch.randn((1, TOKENS, 3, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    return linears, (q, k, v)
+
+
+class Timers:
+    """Per-kernel HIP event pairs recorded on the launching (current) stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs: dict[str, list] = {}
+
+    def start(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        return name, e
+
+    def stop(self, tok):
+        name, s = tok
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.setdefault(name, []).append((s, e))
+
+    def mean_ms(self):
+        return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
+
+
+def run_step(torch, ops, linears, qkv, timers: Timers | None):
+    """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make."""
+    tick = timers.start if timers else (lambda n: None)
+    tock = timers.stop if timers else (lambda t: None)
+    outs = []
+    for name, mod, x in linears:
+        t = tick(f"quant_rows[{name}]")
+        x8, sa = ops.quant_rows(x)
+        tock(t)
+        t = tick(f"gemm[{name}]")
+        outs.append(ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), None, None, 0.0))
+        tock(t)
+    q, k, v = qkv
+    t = tick("attn_quant_q")
+    q8, sq = ops.attn_quant_q(q, ops.softmax_c(None, HEAD_DIM))
+    tock(t)
+    t = tick("attn_kmean+quant_k")
+    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+    tock(t)
+    t = tick("attn_quant_v")
+    v8t, sv = ops.attn_quant_v(v)
+    tock(t)
+    t = tick("attn_fwd")
+    outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, TOKENS))
+    tock(t)
+    return outs
+
+
+def cpu_baseline(target_s: float = 12.0) -> dict:
+    """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix."""
+    import torch
+
+    from oracle.cpu_baseline import dequant_linear, quantize_rows_torch, sdpa_fallback
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    ms = 512
+    lin = []
+    for _, k, n, _ in LINEARS:
+        x = torch.randn((ms, k), generator=g).to(torch.bfloat16)
+        w = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16)
+        x8, sa = quantize_rows_torch(x)
+        w8, sw = quantize_rows_torch(w)
+        lin.append((x8, sa, w8, sw.view(1, -1), (torch.randn((n,), generator=g) * 0.01).to(torch.bfloat16)))
+    lin_flops = sum(gemm_flops(ms, n, k) for _, k, n, _ in LINEARS)
+    hs = 1
+    q, k, v = (torch.randn((1, hs, TOKENS, HEAD_DIM), generator=g) for _ in range(3))
+    at_flops = attn_flops(1, hs, TOKENS, TOKENS, HEAD_DIM)
+
+    def timed(fn, budget):
+        fn()  # warmup
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or reps >= 50:
+                return el / reps
+
+    t_lin = timed(lambda: [dequant_linear(*a) for a in lin], target_s / 2)
+    t_att = timed(lambda: sdpa_fallback(q, k, v), target_s / 2)
+    lin_rate, att_rate = lin_flops / t_lin, at_flops / t_att
+    step_lin = sum(gemm_flops(TOKENS, n, k) for _, k, n, _ in LINEARS)
+    step_att = attn_flops(1, HEADS, TOKENS, TOKENS, HEAD_DIM)
+    step_s = step_lin / lin_rate + step_att / att_rate
+    return {
+        "value": round((step_lin + step_att) / step_s / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch CPU fp32 dequant-matmul of the 4 DiT linears on {ms} of {TOKENS} tokens "
+                   f"({lin_rate / 1e12:.3f} TFLOP/s) and fp32 SDPA on {hs} of {HEADS} heads at S={TOKENS} "
+                   f"({att_rate / 1e12:.3f} TFLOP/s); value = the step's FLOPs over the step time these "
+                   f"rates imply ({step_s:.1f} s); host {platform.processor() or platform.machine()}, "
+                   f"{cores} threads"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from minimaxh3_amd import _native, ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _native.load()
+    _native.require_gfx950(dev)
+    log("[bench] building workload")
+    linears, qkv = build_workload(torch, dev)
+    torch.cuda.synchronize()
+
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            run_step(torch, ops, linears, qkv, None)
+        torch.cuda.synchronize()
+        log(f"[bench] warmup done ({args.warmup} steps)")
+        timers = Timers(torch)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run_step(torch, ops, linears, qkv, timers)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
+    ms_step = elapsed * 1e3 / args.steps
+    kern = timers.mean_ms()
+
+    step_flops = 0.0
+    parts = {}
+    for name, k, n, _ in LINEARS:
+        f = gemm_flops(TOKENS, n, k)
+        step_flops += f
+        t = kern[f"gemm[{name}]"]
+        parts[f"gemm[{name}]"] = {"ms": round(t, 4), "TFLOP/s": round(f / t / 1e9, 1),
+                                  "frac": round(f / t / 1e9 / PEAK_FP8_TFLOPS, 4)}
+        qb = TOKENS * k * 3 + TOKENS * 4        # bf16 read + e4m3 write + fp32 scales
+        t = kern[f"quant_rows[{name}]"]
+        parts[f"quant_rows[{name}]"] = {"ms": round(t, 4), "GB/s": round(qb / t / 1e6, 1),
+                                        "frac": round(qb / t / 1e6 / PEAK_HBM_GBS, 4)}
+    af = attn_flops(1, HEADS, TOKENS, TOKENS, HEAD_DIM)
+    step_flops += af
+    t_attn = kern["attn_fwd"]
+    parts["attn_fwd"] = {"ms": round(t_attn, 4), "TFLOP/s": round(af / t_attn / 1e9, 1),
+                         "frac": round(af / t_attn / 1e9 / PEAK_FP8_TFLOPS, 4)}
+    nelem = HEADS * TOKENS * HEAD_DIM
+    for name, nscale in (("attn_quant_q", HEADS * math.ceil(TOKENS / 128)),
+                         ("attn_kmean+quant_k", HEADS * math.ceil(TOKENS / 128)),
+                         ("attn_quant_v", HEADS * HEAD_DIM)):
+        qb = 3 * nelem + 4 * nscale
+        t = kern[name]
+        parts[name] = {"ms": round(t, 4), "GB/s": round(qb / t / 1e6, 1),
+                       "frac": round(qb / t / 1e6 / PEAK_HBM_GBS, 4)}
+    gemm_f = step_flops - af
+    gemm_ms = sum(kern[f"gemm[{n}]"] for n, *_ in LINEARS)
+    value = step_flops / (ms_step * 1e-3) / 1e12
+    achieved = af / (t_attn * 1e-3) / 1e12
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 (fp32 accumulate)",
+        "data": "synthetic (seeded randn, random-init weights)",
+        "config": {
+            "workload": "DiT block FP8 hot path at 480p: 4 FP8 linears (M=20280, hidden 3072, MLP 12288, "
+                        "GELU-tanh on MLP-up) + FP8 flash-attention B=1 H=24 S=20280 D=128",
+            "tokens": TOKENS, "hidden": HIDDEN, "mlp": MLP, "heads": HEADS, "head_dim": HEAD_DIM,
+            "step_tflop": round(step_flops / 1e12, 4),
+        },
+        "frac_of_fp8_peak": round(value / PEAK_FP8_TFLOPS, 4),
+        "gemm_tflops": round(gemm_f / (gemm_ms * 1e-3) / 1e12, 1),
+        "attn_tflops": round(achieved, 1),
+        "roofline": {
+            "kernel": "attn_fwd_kernel<128,false,false,false,bf16>",
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+            "traffic": None,
+        },
+        "kernels": parts,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline")
+        line["cpu_baseline"] = cpu_baseline()
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

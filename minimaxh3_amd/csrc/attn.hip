@@ -11,7 +11,7 @@ extern "C" int mxf8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t
     return set_error(MXF8_EINVAL, "attn_fwd: null pointer");
   if (D != 64 && D != 128) return set_error(MXF8_EINVAL, "attn_fwd: D must be 64 or 128");
   if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0) return set_error(MXF8_EINVAL, "attn_fwd: empty shape");
-  if (B * H > 65535) return set_error(MXF8_EINVAL, "attn_fwd: B*H must be <= 65535");
+  if (cdiv(Sq, 128) * B * H >= ((int64_t)1 << 31)) return set_error(MXF8_EINVAL, "attn_fwd: too many Q tiles");
   if (out_dtype != MXF8_BF16 && out_dtype != MXF8_F16) return set_error(MXF8_EINVAL, "attn_fwd: out dtype");
   const int64_t Skp = cdiv(Sk, 128) * 128;
   if (Skp * D >= ((int64_t)1 << 31) || cdiv(Sq, 128) * 128 * D >= ((int64_t)1 << 31))

@@ -2,26 +2,37 @@
 //
 // Algorithm (kernels/fp8_attention.py:215-297, BLOCK_M = BLOCK_N = 128): per (b, h, Q tile
 // I of 128 rows) the KV tiles are visited in the staggered order j = (j0 + i) % nk with
-// j0 = I*nk/nq; scores are in the log2 domain S = (Q8 K8^T) * sq * sk; the row max m is
-// lazy (it moves to the tile max only when that exceeds m + 8, or on the first valid
-// tile); P is produced without exp2 as the e4m3 code rint(8 S + 56 - 8 m) (0 below 8);
-// l += sum(P); O += P V; with repair_tau >= 0, exp2(S - m) - P is added for codes >= tau
-// through bf16.  Output = O * sv / max(l, 1e-12).
+// j0 = I*nk/nq; scores are in the log2 domain S = (Q8 K8^T) * sq * sk (+ bias * log2 e);
+// the row max m is lazy (it moves to the tile max only when that exceeds m + 8, or while
+// m is still -1e9); P is produced without exp2 as the e4m3 code rint(8 S + 56 - 8 m)
+// (0 below 8); l += sum(P); O += P V; with repair_tau >= 0, exp2(S - m) - P is added for
+// codes >= tau through bf16.  Output = O * sv / max(l, 1e-12).
 //
-// Mapping to CDNA4.  A workgroup (4 waves) owns one Q tile; wave w owns its 32 rows.  The
+// Mapping to CDNA4.  A workgroup (4 waves) owns one Q tile; wave w owns its 32 rows, and
+// two workgroups share a CU (the kernel is register-limited to 256 VGPRs per lane) so that
+// one wave's softmax (VALU) overlaps the other's matrix products on each SIMD.  The
 // kernel computes the TRANSPOSED score tile S^T = K Q^T with v_mfma_f32_32x32x64_f8f6f4:
-// in the 32x32 accumulator layout lane l holds query column l%32, so every softmax row
+// in the 32x32 accumulator layout lane l holds query column l%32, so every per-query
 // statistic is lane-local (plus one exchange with lane l^32).  The K rows of each 32-key
 // subtile are fed to the MFMA in a permuted order chosen so that the accumulator
-// registers, packed 4 per dword, ARE the B operand of the PV MFMA (O^T = V^T P^T) with
-// V^T read as contiguous 32-byte runs of a v8t row: no cross-lane shuffles between the
-// two products.  K and V^T tiles (and the mask / bias of the tile) are copied global ->
-// LDS by the direct-to-LDS DMA, double-buffered.
+// registers, packed 4 codes per dword, ARE the B operand of the PV MFMA (O^T = V^T P^T)
+// with V^T read as contiguous 32-byte runs of a v8t row: no cross-lane shuffles between
+// the two products.  The row sums l come from the matrix cores too: one more MFMA per
+// 64 keys with an all-ones A operand.  K and V^T tiles (and the mask / bias of the tile)
+// are copied global -> LDS by the direct-to-LDS DMA into two buffers; one barrier per
+// tile both publishes tile i and retires the buffer that tile i+1 is loaded into.
+//
+// Per score the VALU does: one max (3-input), one FMA (8 S + 56 - 8 m straight from the
+// fp32 dot product with the per-tile constant 8 sq sk), a compare, a round, a select and
+// a byte pack.  Folding sq * sk into one constant rounds 8 S once instead of twice; the
+// row max that drives the lazy-max policy is still computed exactly as (max * sq) * sk.
 #pragma once
 
 #include "common.h"
 
 namespace mxf8 {
+
+constexpr float kAttnNeg = -1.0e9f;
 
 __device__ __forceinline__ void attn_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -29,23 +40,24 @@ __device__ __forceinline__ void attn_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Key (within a 128-key tile) of accumulator row R of score subtile t, and of register i
-// of lane group g.  Subtile t covers keys 64(t/2) + 16(t%2) + {0..15, 32..47}.
+// Key (within a 128-key tile) of accumulator row R of score subtile t.  Subtile t covers
+// keys 64(t/2) + 16(t%2) + {0..15, 32..47}; register i of lane group g of subtile t then
+// holds key 64(t/2) + 32g + 16(t%2) + i, i.e. the byte order of the PV B operand.
 __host__ __device__ constexpr int key_of_row(int t, int R) {
   return 64 * (t >> 1) + 16 * (t & 1) + 32 * ((R >> 2) & 1) + 4 * (R >> 3) + (R & 3);
 }
 
-template <int D>
+template <int D, bool AUX>
 struct AttnTile {
-  static constexpr int KB = 128 * D;    // K tile bytes (128 keys x D)
-  static constexpr int VB = D * 128;    // V^T tile bytes (D rows x 128 keys)
-  static constexpr int AUXB = 2048;     // bias (1 KB slot) + mask (1 KB slot)
-  static constexpr int CPRK = D / 16;   // 16-byte chunks per K row
-  static constexpr int K_INSTR = KB / 1024 / 4;  // DMA instructions per wave
+  static constexpr int KB = 128 * D;             // K tile bytes (128 keys x D)
+  static constexpr int VB = D * 128;             // V^T tile bytes (D rows x 128 keys)
+  static constexpr int AUXB = AUX ? 2048 : 0;    // bias (1 KB) + mask (1 KB)
+  static constexpr int BUF = KB + VB + AUXB;     // one LDS buffer
+  static constexpr int CPRK = D / 16;            // 16-byte chunks per K row
+  static constexpr int K_INSTR = KB / 1024 / 4;  // 1 KB DMA instructions per wave
   static constexpr int V_INSTR = VB / 1024 / 4;
 };
 
-template <int D>
 __device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int row_bytes, int cpr, int chunk0) {
   const int sw = row & (cpr - 1);
   const v4i lo = *reinterpret_cast<const v4i*>(tile + row * row_bytes + ((chunk0 ^ sw) << 4));
@@ -56,19 +68,20 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int row_
   return r;
 }
 
-// DMA one KV tile (keys [kv0, kv0 + 128)) of head bh into LDS buffers.
+// DMA one KV tile (keys [kv0, kv0 + 128)) of head bh into the LDS buffer `buf`.
 template <int D, bool HAS_MASK, bool HAS_BIAS>
 __device__ __forceinline__ void attn_dma(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
-                                         __amdgpu_buffer_rsrc_t brs, __amdgpu_buffer_rsrc_t mrs, uint8_t* sK,
-                                         uint8_t* sV, uint8_t* sAux, uint32_t k_lane, uint32_t v_lane, int wave,
-                                         int lane, int kv0, int Skp, int Sk, const float* bias_row,
-                                         const uint8_t* mask_row) {
-  typedef AttnTile<D> T;
-  constexpr int RPI = 64 / T::CPRK;  // K rows per 1 KB instruction
+                                         __amdgpu_buffer_rsrc_t brs, __amdgpu_buffer_rsrc_t mrs, uint8_t* buf,
+                                         uint32_t k_lane, uint32_t v_lane, int wave, int lane, int kv0, int Skp,
+                                         int Sk, const float* bias_row, const uint8_t* mask_row) {
+  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+  uint8_t* sK = buf;
+  uint8_t* sV = buf + T::KB;
+  uint8_t* sAux = buf + T::KB + T::VB;
 #pragma unroll
   for (int j = 0; j < T::K_INSTR; ++j) {
     const int J = wave * T::K_INSTR + j;
-    // LDS rows [RPI*J, RPI*J + RPI): accumulator row R of subtile t = R/32 loads key key_of_row.
+    // LDS rows of instruction J: accumulator row R of subtile t = R/32 loads key key_of_row.
     int ubase;
     if constexpr (D == 128) {
       const int t = J >> 2;
@@ -123,23 +136,34 @@ __device__ __forceinline__ void attn_dma(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
   }
 }
 
-template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR>
+template <int D, bool DO_REPAIR>
 struct AttnState {
   static constexpr int NDT = D / 32;  // O^T row tiles
   v16f o[NDT];
   v16f orep[DO_REPAIR ? NDT : 1];
-  float m, l;
+  v16f lacc;     // every register holds the running sum of P codes of the lane's query
+  float m;       // lazy row max (log2 domain)
+  float ldelta;  // repair: running sum of the exact-minus-code corrections (lane's keys)
 };
 
-// Process one KV tile held in LDS.
+// e4m3 value of a P code (codes are 0 or in [8, 126], i.e. zero or normal).
+__device__ __forceinline__ float p_value(uint32_t code) {
+  return code ? __uint_as_float((code << 20) + 0x3C000000u) : 0.0f;
+}
+
+// Process one KV tile held in LDS buffer `buf`.
 template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR>
-__device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, const uint8_t* sAux,
-                                          const v8i (&qf)[D / 64], float sq, float skj, int kv0, int Sk,
-                                          float tau, int lane, AttnState<D, HAS_MASK, HAS_BIAS, DO_REPAIR>& st) {
+__device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D / 64], float sq, float skj, int kv0,
+                                          int Sk, float tau, int lane, AttnState<D, DO_REPAIR>& st) {
+  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
   constexpr int NDT = D / 32;
-  constexpr float NEG = -1.0e9f;
+  constexpr float LOG2E_F = 1.4426950408889634f;
+  const uint8_t* sK = buf;
+  const uint8_t* sV = buf + T::KB;
+  const uint8_t* sAux = buf + T::KB + T::VB;
   const int g = lane >> 5;
-  // ---- S^T = K Q^T (4 subtiles of 32 keys x 32 queries)
+
+  // ---- S^T = K Q^T (4 subtiles of 32 keys x 32 queries); s[t][i] is key 64(t/2) + 32g + 16(t%2) + i
   v16f s[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -147,55 +171,58 @@ __device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, 
     for (int i = 0; i < 16; ++i) s[t][i] = 0.0f;
 #pragma unroll
     for (int h = 0; h < D / 64; ++h) {
-      const v8i kf = lds_read32<D>(sK, 32 * t + (lane & 31), D, D / 16, 4 * h + 2 * g);
+      const v8i kf = lds_read32(sK, 32 * t + (lane & 31), D, D / 16, 4 * h + 2 * g);
       s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf[h], s[t], 0, 0, 0, 0, 0, 0);
     }
   }
-  // ---- scale, bias, validity; s[t][i] is key 64(t/2) + 16(t%2) + 32g + i of the tile
-  const bool full = (kv0 + 128 <= Sk) && !HAS_MASK && !HAS_BIAS;
-  uint64_t validbits = ~0ull;  // bit 16t + i
-  float rmax = NEG;
+
+  // ---- scores of invalid keys become -inf; with a bias, S is formed explicitly
+  const bool partial = kv0 + 128 > Sk;
+  if (HAS_MASK || HAS_BIAS || partial) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
-    float bias[16];
-    if constexpr (HAS_BIAS) {
+    for (int t = 0; t < 4; ++t) {
+      const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
+      float bias[16];
+      if constexpr (HAS_BIAS) {
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const v4f b4 = *reinterpret_cast<const v4f*>(sAux + (kb + 4 * q4) * 4);
-        bias[4 * q4 + 0] = b4[0]; bias[4 * q4 + 1] = b4[1]; bias[4 * q4 + 2] = b4[2]; bias[4 * q4 + 3] = b4[3];
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const v4f b4 = *reinterpret_cast<const v4f*>(sAux + (kb + 4 * q4) * 4);
+          bias[4 * q4 + 0] = b4[0]; bias[4 * q4 + 1] = b4[1]; bias[4 * q4 + 2] = b4[2]; bias[4 * q4 + 3] = b4[3];
+        }
       }
-    }
-    uint32_t mbytes[4] = {~0u, ~0u, ~0u, ~0u};
-    if constexpr (HAS_MASK) {
-      const v4i m4 = *reinterpret_cast<const v4i*>(sAux + 1024 + kb);
-      mbytes[0] = m4[0]; mbytes[1] = m4[1]; mbytes[2] = m4[2]; mbytes[3] = m4[3];
-    }
+      uint32_t mbytes[4] = {~0u, ~0u, ~0u, ~0u};
+      if constexpr (HAS_MASK) {
+        const v4i m4 = *reinterpret_cast<const v4i*>(sAux + 1024 + kb);
+        mbytes[0] = m4[0]; mbytes[1] = m4[1]; mbytes[2] = m4[2]; mbytes[3] = m4[3];
+      }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float v = (s[t][i] * sq) * skj;
-      if (!full) {
+      for (int i = 0; i < 16; ++i) {
         bool ok = kv0 + kb + i < Sk;
+        float v = s[t][i];
         if constexpr (HAS_BIAS) {
           ok = ok && (bias[i] > -1.0e8f);
-          v = v + bias[i] * 1.4426950408889634f;
+          v = (v * sq) * skj + bias[i] * LOG2E_F;
         }
         if constexpr (HAS_MASK) ok = ok && (((mbytes[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0u);
-        if (!ok) {
-          v = NEG;
-          validbits &= ~(1ull << (16 * t + i));
-        }
+        s[t][i] = ok ? v : -INFINITY;
       }
-      s[t][i] = v;
-      rmax = fmaxf(rmax, v);
     }
   }
-  rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+
+  // ---- row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float rmax = fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
+
   // ---- lazy max
   const float m_old = st.m;
-  const float m_new = (rmax > m_old + 8.0f || m_old == NEG) ? rmax : m_old;
-  const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // wave-uniform: skip when no row moved
+  const float m_new = (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
+  if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {  // wave-uniform: skip when no row moved
+    const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -205,15 +232,23 @@ __device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, 
         for (int i = 0; i < 16; ++i) st.orep[dt][i] *= alpha;
       }
     }
-    st.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st.lacc[i] *= alpha;
+    if constexpr (DO_REPAIR) st.ldelta *= alpha;
   }
   st.m = m_new;
-  // ---- exp2-free P codes, row sum, packing into the PV B operand
+
+  // ---- exp2-free P codes: code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m.  bits
+  // never exceeds 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's
+  // clamp to [0, 126] is inactive.  v_cvt_pk_u8_f32 rounds to nearest even and saturates
+  // negative inputs to 0, so it performs rint itself; the flush below 8 is
+  // min(bits, (bits - 8) * 2^24), negative exactly when bits < 8 and equal to bits when
+  // bits >= 8 + 2^-21.  Invalid keys carry S = -inf and flush to 0.
   const float cst = 56.0f - 8.0f * m_new;
+  const float c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
+  const float c8f = c8 * 16777216.0f;
+  const float cstf = (48.0f - 8.0f * m_new) * 16777216.0f;
   v8i pf[2];
-  float lsum = 0.0f;
-  float pexact[DO_REPAIR ? 64 : 1];
-  float papx[DO_REPAIR ? 64 : 1];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -221,32 +256,26 @@ __device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, 
       uint32_t word = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = 4 * w4 + e;
-        const float bits = __builtin_fmaf(s[t][i], 8.0f, cst);
-        const bool valid = (validbits >> (16 * t + i)) & 1ull;
-        const float code = (bits < 8.0f || !valid) ? 0.0f : fminf(fmaxf(__builtin_rintf(bits), 0.0f), 126.0f);
-        word = __builtin_amdgcn_cvt_pk_u8_f32(code, e, word);
-        const uint32_t ci = (uint32_t)code;
-        const float p = ci ? __uint_as_float((ci << 20) + 0x3C000000u) : 0.0f;
-        lsum += p;
-        if constexpr (DO_REPAIR) {
-          papx[16 * t + i] = p;
-          pexact[16 * t + i] = valid ? __builtin_amdgcn_exp2f(s[t][i] - m_new) : 0.0f;
-        }
+        const float bits = __builtin_fmaf(s[t][4 * w4 + e], c8, cst);
+        const float flush = __builtin_fmaf(s[t][4 * w4 + e], c8f, cstf);
+        word = __builtin_amdgcn_cvt_pk_u8_f32(fminf(bits, flush), e, word);
       }
       pf[t >> 1][4 * (t & 1) + w4] = (int)word;
     }
   }
-  st.l += lsum;
-  // ---- O^T += V^T P^T
+
+  // ---- O^T += V^T P^T, l += 1^T P^T
+  const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
+  for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      const v8i vf = lds_read32<D>(sV, 32 * dt + (lane & 31), 128, 8, 4 * kh + 2 * g);
+    for (int dt = 0; dt < NDT; ++dt) {
+      const v8i vf = lds_read32(sV, 32 * dt + (lane & 31), 128, 8, 4 * kh + 2 * g);
       st.o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf[kh], st.o[dt], 0, 0, 0, 0, 0, 0);
     }
+    st.lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
   }
+
   if constexpr (DO_REPAIR) {
     // delta = exp2(S - m) - P where P >= tau; O_r^T += bf16(V^T) bf16(delta^T) over 16-key
     // chunks: chunk (t, u) gives lane group g the 8 keys 64(t/2) + 16(t%2) + 32g + 8u + 0..7.
@@ -258,8 +287,12 @@ __device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, 
         v8bf db;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int i = 16 * t + 8 * u + e;
-          const float d = (papx[i] >= tau) ? (pexact[i] - papx[i]) : 0.0f;
+          const int i = 8 * u + e;
+          const uint32_t code = ((uint32_t)pf[t >> 1][4 * (t & 1) + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
+          const float papx = p_value(code);
+          const float S = HAS_BIAS ? s[t][i] : (s[t][i] * sq) * skj;
+          const float pexact = __builtin_amdgcn_exp2f(S - m_new);  // invalid keys: S = -inf -> 0
+          const float d = (papx >= tau) ? (pexact - papx) : 0.0f;
           dsum += d;
           db[e] = __builtin_bit_cast(__bf16, (unsigned short)f32_to_bf16_bits(d));
         }
@@ -289,31 +322,40 @@ __device__ __forceinline__ void attn_tile(const uint8_t* sK, const uint8_t* sV, 
         }
       }
     }
-    st.l += dsum;
+    st.ldelta += dsum;
   }
 }
 
-template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8,
-                                                       const uint8_t* __restrict__ v8t, const float* __restrict__ sq,
-                                                       const float* __restrict__ sk, const float* __restrict__ sv,
-                                                       const uint8_t* __restrict__ key_mask,
-                                                       const float* __restrict__ key_bias, float tau,
-                                                       void* __restrict__ out, int64_t os_b, int64_t os_h,
-                                                       int64_t os_s, int64_t os_d, int H, int Sq, int Sk) {
-  typedef AttnTile<D> T;
-  constexpr int NDT = D / 32;
-  __shared__ __attribute__((aligned(1024))) uint8_t sK0[T::KB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV0[T::VB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sA0[(HAS_MASK || HAS_BIAS) ? T::AUXB : 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t sK1[T::KB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV1[T::VB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sA1[(HAS_MASK || HAS_BIAS) ? T::AUXB : 16];
+// Register budget: 256 VGPRs per lane (two waves per SIMD) for the plain kernel; the
+// repair variant keeps S, codes and the correction accumulator live and runs one wave.
+template <bool DO_REPAIR>
+struct AttnOccupancy {
+  static constexpr int waves = DO_REPAIR ? 1 : 2;
+};
 
-  const int I = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / H, h = bh % H;
-  const int nq = gridDim.x;
+template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOccupancy<DO_REPAIR>::waves)))
+void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
+                     const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
+                     const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
+                     void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H, int Sq,
+                     int Sk, int nq) {
+  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+  constexpr int NDT = D / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * T::BUF];
+
+  // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous range of
+  // (head, Q tile) ids so that the workgroups resident on one XCD are consecutive Q tiles
+  // of one head, whose staggered KV sweeps overlap and share that XCD's L2.
+  int bh, I;
+  {
+    const int total = gridDim.x, L = blockIdx.x;
+    const int q = total >> 3, r = total & 7, x = L & 7, kk = L >> 3;
+    const int id = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + kk;
+    bh = id / nq;
+    I = id - bh * nq;
+  }
+  const int b = bh / H, h = bh - (bh / H) * H;
   const int nk = (Sk + 127) / 128;
   const int Sqp = nq * 128, Skp = nk * 128;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -354,13 +396,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const uint8_t* __restrict
   } else {
     // 64-byte rows: lane i: LDS row 16J + i/4, phys chunk i%4 -> logical (i%4) ^ ((i/4)&3)
     const int rr = lane >> 2;  // row within the 16-row instruction, R = 16(J&1) + rr
-    k_lane = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D +
-                        (((lane & 3) ^ (rr & 3)) << 4));
+    k_lane = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D + (((lane & 3) ^ (rr & 3)) << 4));
   }
   const uint32_t v_lane = (uint32_t)((lane >> 3) * Skp + (((lane & 7) ^ (lane >> 3)) << 4));
-  constexpr int PER_TILE = T::K_INSTR + T::V_INSTR;
 
-  AttnState<D, HAS_MASK, HAS_BIAS, DO_REPAIR> st;
+  AttnState<D, DO_REPAIR> st;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -368,48 +408,34 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const uint8_t* __restrict
       st.o[dt][i] = 0.0f;
       if constexpr (DO_REPAIR) st.orep[dt][i] = 0.0f;
     }
-  st.m = -1.0e9f;
-  st.l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) st.lacc[i] = 0.0f;
+  st.m = kAttnNeg;
+  st.ldelta = 0.0f;
 
   const int j0 = (int)(((int64_t)I * nk) / nq);
-  auto jof = [&](int i) { int j = j0 + i; return j >= nk ? j - nk : j; };
-
-  attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, sK0, sV0, sA0, k_lane, v_lane, wave, lane, jof(0) * 128, Skp, Sk, brow, mrow);
-  int i = 0;
-  for (; i + 2 < nk; i += 2) {
-    const int ja = jof(i), jb = jof(i + 1);
-    attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, sK1, sV1, sA1, k_lane, v_lane, wave, lane, jb * 128, Skp, Sk, brow, mrow);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_TILE) : "memory");
+  attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, smem, k_lane, v_lane, wave, lane, j0 * 128, Skp, Sk, brow,
+                                  mrow);
+  int j = j0;
+  for (int i = 0; i < nk; ++i) {
+    // Tile i is the only DMA in flight; after the barrier every wave has finished tile
+    // i-1, so its buffer can take tile i+1 while tile i is computed.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     attn_barrier();
-    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(sK0, sV0, sA0, qf, sqI, skh[ja], ja * 128, Sk, tau, lane, st);
-    attn_barrier();
-    attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, sK0, sV0, sA0, k_lane, v_lane, wave, lane, jof(i + 2) * 128,
-                                    Skp, Sk, brow, mrow);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_TILE) : "memory");
-    attn_barrier();
-    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(sK1, sV1, sA1, qf, sqI, skh[jb], jb * 128, Sk, tau, lane, st);
-    attn_barrier();
-  }
-  const bool two_left = i + 1 < nk;
-  if (two_left) {
-    const int ja = jof(i), jb = jof(i + 1);
-    attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, sK1, sV1, sA1, k_lane, v_lane, wave, lane, jb * 128, Skp, Sk, brow, mrow);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_TILE) : "memory");
-    attn_barrier();
-    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(sK0, sV0, sA0, qf, sqI, skh[ja], ja * 128, Sk, tau, lane, st);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  attn_barrier();
-  {
-    const int jl = jof(two_left ? i + 1 : i);
-    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(two_left ? sK1 : sK0, two_left ? sV1 : sV0, two_left ? sA1 : sA0, qf,
-                                                sqI, skh[jl], jl * 128, Sk, tau, lane, st);
+    const int jn = j + 1 == nk ? 0 : j + 1;
+    if (i + 1 < nk)
+      attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, smem + ((i + 1) & 1) * T::BUF, k_lane, v_lane, wave, lane,
+                                      jn * 128, Skp, Sk, brow, mrow);
+    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(smem + (i & 1) * T::BUF, qf, sqI, skh[j], j * 128, Sk, tau, lane,
+                                                st);
+    j = jn;
   }
 
   // ---- epilogue: O = (O + O_r) * sv / max(l, 1e-12); lane holds query qrow, channels
   // 32 dt + 8 (i/4) + 4 g + i%4
-  const float l = st.l + __shfl_xor(st.l, 32, 64);
   if (qrow >= Sq) return;
+  float l = st.lacc[0];
+  if constexpr (DO_REPAIR) l += st.ldelta + __shfl_xor(st.ldelta, 32, 64);
   const float den = fmaxf(l, 1.0e-12f);
   const float* svh = sv + (int64_t)bh * D;
   char* obase = static_cast<char*>(out) + ((int64_t)b * os_b + (int64_t)h * os_h + (int64_t)qrow * os_s) * 2;
@@ -418,12 +444,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d0 = 32 * dt + 8 * q4 + 4 * g;
+      const v4f sv4 = *reinterpret_cast<const v4f*>(svh + d0);
       uint32_t ob[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float acc = st.o[dt][4 * q4 + e];
         if constexpr (DO_REPAIR) acc += st.orep[dt][4 * q4 + e];
-        const float v = __fdiv_rn(acc * svh[d0 + e], den);
+        const float v = __fdiv_rn(acc * sv4[e], den);
         ob[e] = ODT == MXF8_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
       }
       uint16_t* dst = reinterpret_cast<uint16_t*>(obase) + (int64_t)d0 * os_d;
@@ -441,9 +468,10 @@ template <int D, bool M_, bool B_, bool R_, int ODT>
 static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t, const float* sq, const float* sk,
                         const float* sv, const uint8_t* km, const float* kb, float tau, void* out,
                         const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, hipStream_t st) {
-  dim3 grid((unsigned)cdiv(Sq, 128), (unsigned)(B * H));
+  const int64_t nq = cdiv(Sq, 128);
+  dim3 grid((unsigned)(nq * B * H));
   attn_fwd_kernel<D, M_, B_, R_, ODT><<<grid, 256, 0, st>>>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1],
-                                                            os[2], os[3], (int)H, (int)Sq, (int)Sk);
+                                                            os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq);
 }
 
 template <int D, int ODT>

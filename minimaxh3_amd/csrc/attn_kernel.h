@@ -22,10 +22,11 @@
 // are copied global -> LDS by the direct-to-LDS DMA into two buffers; one barrier per
 // tile both publishes tile i and retires the buffer that tile i+1 is loaded into.
 //
-// Per score the VALU does: one max (3-input), one FMA (8 S + 56 - 8 m straight from the
-// fp32 dot product with the per-tile constant 8 sq sk), a compare, a round, a select and
-// a byte pack.  Folding sq * sk into one constant rounds 8 S once instead of twice; the
-// row max that drives the lazy-max policy is still computed exactly as (max * sq) * sk.
+// Per score the VALU does half a 3-input max, two FMAs (8 S + 56 - 8 m straight from the
+// fp32 dot product with the per-tile constant 8 sq sk, and the same shifted and scaled
+// for the flush test), a min and a rounding byte pack.  Folding sq * sk into one constant
+// rounds 8 S once instead of twice; the row max that drives the lazy-max policy is still
+// computed exactly as (max * sq) * sk.
 #pragma once
 
 #include "common.h"
@@ -58,10 +59,12 @@ struct AttnTile {
   static constexpr int V_INSTR = VB / 1024 / 4;
 };
 
-__device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int row_bytes, int cpr, int chunk0) {
-  const int sw = row & (cpr - 1);
-  const v4i lo = *reinterpret_cast<const v4i*>(tile + row * row_bytes + ((chunk0 ^ sw) << 4));
-  const v4i hi = *reinterpret_cast<const v4i*>(tile + row * row_bytes + (((chunk0 + 1) ^ sw) << 4));
+// 32 bytes = logical chunks chunk0, chunk0 + 1 of `row` of a swizzled tile.
+template <int ROW_BYTES>
+__device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int chunk0) {
+  const int sw = lds_swz<ROW_BYTES>(row);
+  const v4i lo = *reinterpret_cast<const v4i*>(tile + row * ROW_BYTES + ((chunk0 ^ sw) << 4));
+  const v4i hi = *reinterpret_cast<const v4i*>(tile + row * ROW_BYTES + (((chunk0 + 1) ^ sw) << 4));
   v8i r;
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
   r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
@@ -72,7 +75,8 @@ __device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int row_
 template <int D, bool HAS_MASK, bool HAS_BIAS>
 __device__ __forceinline__ void attn_dma(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
                                          __amdgpu_buffer_rsrc_t brs, __amdgpu_buffer_rsrc_t mrs, uint8_t* buf,
-                                         uint32_t k_lane, uint32_t v_lane, int wave, int lane, int kv0, int Skp,
+                                         const uint32_t (&k_lane)[2], const uint32_t (&v_lane)[2], int wave, int lane,
+                                         int kv0, int Skp,
                                          int Sk, const float* bias_row, const uint8_t* mask_row) {
   typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
   uint8_t* sK = buf;
@@ -90,12 +94,14 @@ __device__ __forceinline__ void attn_dma(__amdgpu_buffer_rsrc_t krs, __amdgpu_bu
       const int t = J >> 1;
       ubase = 64 * (t >> 1) + 16 * (t & 1) + 8 * (J & 1);
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, LDS_PTR(sK + J * 1024), 16, k_lane, (kv0 + ubase) * D, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, LDS_PTR(sK + J * 1024), 16, k_lane[j & 1], (kv0 + ubase) * D, 0,
+                                             0);
   }
 #pragma unroll
   for (int j = 0; j < T::V_INSTR; ++j) {
     const int J = wave * T::V_INSTR + j;  // V^T rows [8J, 8J + 8)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, LDS_PTR(sV + J * 1024), 16, v_lane, 8 * J * Skp + kv0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, LDS_PTR(sV + J * 1024), 16, v_lane[j & 1], 8 * J * Skp + kv0, 0,
+                                             0);
   }
   // Mask / bias of the tile.  Full tiles use the DMA; the partial last tile loads element by
   // element with a bounds check (a 16-byte DMA chunk that straddles the end of a [B, Sk]
@@ -171,7 +177,7 @@ __device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D 
     for (int i = 0; i < 16; ++i) s[t][i] = 0.0f;
 #pragma unroll
     for (int h = 0; h < D / 64; ++h) {
-      const v8i kf = lds_read32(sK, 32 * t + (lane & 31), D, D / 16, 4 * h + 2 * g);
+      const v8i kf = lds_read32<D>(sK, 32 * t + (lane & 31), 4 * h + 2 * g);
       s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf[h], s[t], 0, 0, 0, 0, 0, 0);
     }
   }
@@ -270,7 +276,7 @@ __device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D 
   for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      const v8i vf = lds_read32(sV, 32 * dt + (lane & 31), 128, 8, 4 * kh + 2 * g);
+      const v8i vf = lds_read32<128>(sV, 32 * dt + (lane & 31), 4 * kh + 2 * g);
       st.o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf[kh], st.o[dt], 0, 0, 0, 0, 0, 0);
     }
     st.lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
@@ -301,7 +307,7 @@ __device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D 
         for (int dt = 0; dt < NDT; ++dt) {
           const int row = 32 * dt + (lane & 31);
           const int c = key0 >> 4;
-          const uint8_t* src = sV + row * 128 + ((c ^ (row & 7)) << 4) + (key0 & 15);
+          const uint8_t* src = sV + row * 128 + ((c ^ lds_swz<128>(row)) << 4) + (key0 & 15);
           const v2i raw = *reinterpret_cast<const v2i*>(src);
           v8bf vb;
 #pragma unroll
@@ -389,16 +395,25 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     mrs = __builtin_amdgcn_make_buffer_rsrc((void*)(key_mask + (int64_t)b * Sk), 0, Sk, 0x00020000);
   const float* brow = HAS_BIAS ? key_bias + (int64_t)b * Sk : nullptr;
   const uint8_t* mrow = HAS_MASK ? key_mask + (int64_t)b * Sk : nullptr;
-  uint32_t k_lane;
-  if constexpr (D == 128) {
-    // lane i: LDS row 8J + i/8, phys chunk i%8 -> logical (i%8) ^ (i/8); key part of the lane
-    k_lane = (uint32_t)((32 * ((lane >> 5) & 1) + ((lane >> 3) & 3)) * D + (((lane & 7) ^ (lane >> 3)) << 4));
-  } else {
-    // 64-byte rows: lane i: LDS row 16J + i/4, phys chunk i%4 -> logical (i%4) ^ ((i/4)&3)
-    const int rr = lane >> 2;  // row within the 16-row instruction, R = 16(J&1) + rr
-    k_lane = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D + (((lane & 3) ^ (rr & 3)) << 4));
+  // Per-lane DMA offsets.  A 1 KB DMA instruction J fills LDS bytes [1024 J, +1024): lane i
+  // writes 16 bytes at row 8J + i/8 (128-byte rows) or 16J + i/4 (64-byte rows), physical
+  // chunk i%8 (i%4), which must hold logical chunk phys ^ lds_swz(row); for 128-byte rows
+  // that depends on the parity of J, hence one offset per parity.
+  uint32_t k_lane[2], v_lane[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int vrow = 8 * par + (lane >> 3);  // row of a 128-byte-row tile, mod 16
+    const uint32_t chunk128 = (uint32_t)(((lane & 7) ^ lds_swz<128>(vrow)) << 4);
+    v_lane[par] = (uint32_t)((lane >> 3) * Skp) + chunk128;
+    if constexpr (D == 128) {
+      // key of LDS row 8J + i/8 relative to the instruction's first key (key_of_row)
+      k_lane[par] = (uint32_t)((32 * ((lane >> 5) & 1) + ((lane >> 3) & 3)) * D) + chunk128;
+    } else {
+      const int rr = lane >> 2;  // row within the 16-row instruction, R = 16(J&1) + rr
+      k_lane[par] = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D +
+                               (((lane & 3) ^ lds_swz<64>(rr)) << 4));
+    }
   }
-  const uint32_t v_lane = (uint32_t)((lane >> 3) * Skp + (((lane & 7) ^ (lane >> 3)) << 4));
 
   AttnState<D, DO_REPAIR> st;
 #pragma unroll

@@ -115,4 +115,13 @@ __device__ __forceinline__ float block256_max(float v, float* red4) {
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// LDS tiles with 64- or 128-byte rows are stored as 16-byte chunks, logical chunk c of row
+// r at physical chunk c ^ lds_swz(r).  A ds_read_b128 is served 16 lanes at a time over
+// 64 four-byte banks (256 bytes); when 16 consecutive rows read the same logical chunk,
+// this swizzle puts them on 16 distinct (row within 256 bytes, chunk) bank groups.
+template <int ROW_BYTES>
+__host__ __device__ constexpr int lds_swz(int row) {
+  return (row / (256 / ROW_BYTES)) & (ROW_BYTES / 16 - 1);
+}
+
 }  // namespace mxf8

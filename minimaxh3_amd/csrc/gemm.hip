@@ -7,22 +7,40 @@
 // C^T = W X^T so that a lane of the 32x32 accumulator layout owns one output row m and
 // runs of 4 consecutive output columns n: the epilogue then writes 8-byte bf16 quads.
 //
-// Block tile BM (tokens) x BN (channels) x 128 (K stage), 4 waves in a 2x2 grid, each wave
-// (BM/2) x (BN/2) built from v_mfma_f32_32x32x64_f8f6f4.  Operand tiles are copied
+// Block tile BM (tokens) x BN (channels) x 128 (K stage) on WM x WN waves, each wave
+// (BM/WM) x (BN/WN) built from v_mfma_f32_32x32x64_f8f6f4.  The large configuration runs
+// 8 waves on a 256 x 256 tile, two waves per SIMD, so that one wave's LDS reads and
+// barrier waits overlap the other's matrix products.  Operand tiles are copied
 // global -> LDS with the direct-to-LDS DMA (buffer_load_dwordx4 ... lds: 64 lanes x 16
-// bytes into 1 KB of LDS), double-buffered in two separate LDS arrays so the loads of stage
-// k+1 overlap the MFMAs of stage k.  Inside a tile each 128-byte row holds 8 chunks of
-// 16 bytes stored at chunk ^ (row & 7), which makes both the DMA writes and the
-// ds_read_b128 fragment reads bank-conflict free.
+// bytes into 1 KB of LDS) into two stage buffers; one barrier per stage publishes stage
+// k and retires the buffer that stage k+1 is then loaded into, so the copy of stage k+1
+// overlaps the MFMAs of stage k.  Inside a tile each 128-byte row holds 8 chunks of 16
+// bytes stored at chunk ^ lds_swz(row), which makes the ds_read_b128 fragment reads
+// bank-conflict free.
 #include "common.h"
 
 namespace mxf8 {
 
 constexpr int GEMM_BK = 128;
 
+template <int BM_, int BN_, int WM_, int WN_>
+struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int NW = WM * WN;                        // waves per workgroup
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int TM = BM / WM / 32;                   // 32x32 tiles per wave along m
+  static constexpr int TN = BN / WN / 32;                   // along n
+  static constexpr int STAGE = (BM + BN) * GEMM_BK;         // LDS bytes per stage (W tile, then X tile)
+  static constexpr int DMA_PER_WAVE = (BM + BN) / 8 / NW;   // 1 KB DMA instructions per wave per stage
+  static_assert((BN / 8) % DMA_PER_WAVE == 0, "a wave's DMA rows must lie in one operand");
+  static_assert(DMA_PER_WAVE % 2 == 0, "DMA instruction parity must follow the loop index");
+};
+typedef GemmCfg<256, 256, 4, 2> GemmBig;    // 8 waves, 128 KB LDS, one workgroup per CU
+typedef GemmCfg<128, 128, 2, 2> GemmSmall;  // 4 waves, 64 KB LDS, two workgroups per CU
+
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int row, int chunk0) {
   // 32 bytes = logical chunks chunk0, chunk0 + 1 of `row` (swizzled storage)
-  const int sw = row & 7;
+  const int sw = lds_swz<GEMM_BK>(row);
   const v4i lo = *reinterpret_cast<const v4i*>(tile + row * GEMM_BK + ((chunk0 ^ sw) << 4));
   const v4i hi = *reinterpret_cast<const v4i*>(tile + row * GEMM_BK + (((chunk0 + 1) ^ sw) << 4));
   v8i r;
@@ -66,77 +84,83 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Copy ROWS x 128 bytes (rows [row0, row0+ROWS) of a K-contiguous operand, K offset k0)
-// into a swizzled LDS tile; this wave's share is rows [wave*ROWS/4, (wave+1)*ROWS/4).
-// Rows past the end of the operand read as zero (buffer range check).
-template <int ROWS>
-__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, uint32_t lane_off, int K,
-                                         int wave, int k0) {
+// This wave's share of one stage: DMA_PER_WAVE instructions of 8 rows x 128 bytes each,
+// all from one operand (rows past the end of the operand read as zero: buffer range
+// check).  Instruction J fills LDS stage rows [8J, 8J + 8): W rows for J < BN/8, X rows
+// after.  `lane_off` holds the per-lane source offset for even and odd J.
+template <class C>
+__device__ __forceinline__ void gemm_dma(__amdgpu_buffer_rsrc_t wrs, __amdgpu_buffer_rsrc_t xrs, uint8_t* stage,
+                                         const uint32_t (&lane_off)[2], int K, int wave, int k0) {
+  const int J0 = wave * C::DMA_PER_WAVE;
+  const bool is_w = J0 < C::BN / 8;
+  const __amdgpu_buffer_rsrc_t rs = is_w ? wrs : xrs;
+  const int row0 = is_w ? 8 * J0 : 8 * J0 - C::BN;  // first operand row of this wave's share
 #pragma unroll
-  for (int j = 0; j < ROWS / 32; ++j) {
-    const int r = wave * (ROWS / 4) + 8 * j;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, LDS_PTR(lds + r * GEMM_BK), 16,
-                                             lane_off + (uint32_t)(r * K + k0), 0, 0, 0);
+  for (int j = 0; j < C::DMA_PER_WAVE; ++j) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(stage + (J0 + j) * 1024), 16, lane_off[j & 1],
+                                             (row0 + 8 * j) * K + k0, 0, 0);
   }
 }
 
-// Zero the logical 16-byte chunks at or past K (last, partial stage; K % 16 == 0).
-template <int ROWS>
-__device__ __forceinline__ void zero_tail(uint8_t* lds, int valid_chunks) {
-  for (int x = threadIdx.x; x < ROWS * 8; x += 256) {
+// Zero the logical 16-byte chunks at or past K of every row of a stage (last, partial
+// stage; K % 16 == 0).
+template <class C>
+__device__ __forceinline__ void zero_tail(uint8_t* stage, int valid_chunks) {
+  for (int x = threadIdx.x; x < (C::BM + C::BN) * 8; x += C::THREADS) {
     const int row = x >> 3, c = x & 7;
-    if (c >= valid_chunks) *reinterpret_cast<v4i*>(lds + row * GEMM_BK + ((c ^ (row & 7)) << 4)) = v4i{0, 0, 0, 0};
+    if (c >= valid_chunks)
+      *reinterpret_cast<v4i*>(stage + row * GEMM_BK + ((c ^ lds_swz<GEMM_BK>(row)) << 4)) = v4i{0, 0, 0, 0};
   }
 }
 
-template <int TN, int TM>
-__device__ __forceinline__ void mma_stage(const uint8_t* tW, const uint8_t* tX, int wrow0, int xrow0, int lane,
-                                          v16f (&acc)[TN][TM]) {
+template <class C>
+__device__ __forceinline__ void mma_stage(const uint8_t* stage, int wrow0, int xrow0, int lane,
+                                          v16f (&acc)[C::TN][C::TM]) {
+  const uint8_t* tW = stage;
+  const uint8_t* tX = stage + C::BN * GEMM_BK;
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
     const int c0 = 4 * kh + 2 * (lane >> 5);
-    v8i af[TN], bf[TM];
+    v8i af[C::TN], bf[C::TM];
 #pragma unroll
-    for (int t = 0; t < TN; ++t) af[t] = lds_frag(tW, wrow0 + 32 * t + (lane & 31), c0);
+    for (int t = 0; t < C::TN; ++t) af[t] = lds_frag(tW, wrow0 + 32 * t + (lane & 31), c0);
 #pragma unroll
-    for (int t = 0; t < TM; ++t) bf[t] = lds_frag(tX, xrow0 + 32 * t + (lane & 31), c0);
+    for (int t = 0; t < C::TM; ++t) bf[t] = lds_frag(tX, xrow0 + 32 * t + (lane & 31), c0);
 #pragma unroll
-    for (int a = 0; a < TN; ++a)
+    for (int a = 0; a < C::TN; ++a)
 #pragma unroll
-      for (int b = 0; b < TM; ++b)
+      for (int b = 0; b < C::TM; ++b)
         acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf[b], acc[a][b], 0, 0, 0, 0, 0, 0);
   }
 }
 
-template <int BM, int BN, int ACT, bool HAS_LORA, bool KTAIL>
-__global__ __launch_bounds__(256, 1) void gemm_fp8_rowwise_kernel(
+template <class C, int ACT, bool HAS_LORA, bool KTAIL>
+__global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const uint8_t* __restrict__ a8, const uint8_t* __restrict__ w8, const float* __restrict__ sa,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ lora_t,
     const uint16_t* __restrict__ lora_b, int lora_r, float lora_scale, uint16_t* __restrict__ out, int M, int N,
     int K, int64_t ld_out, int tiles_m, int tiles_n) {
-  constexpr int TM = BM / 64;  // 32x32 tiles per wave along m
-  constexpr int TN = BN / 64;  // along n
-  __shared__ __attribute__((aligned(1024))) uint8_t sW0[BN * GEMM_BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t sX0[BM * GEMM_BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t sW1[BN * GEMM_BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t sX1[BM * GEMM_BK];
+  constexpr int TM = C::TM, TN = C::TN;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
 
   int tm, tn;
   tile_coords(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * C::BM, n0 = tn * C::BN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int wn = wave >> 1, wm = wave & 1;
+  const int wn = wave / C::WM, wm = wave % C::WM;
 
-  // DMA: lane i of an 8-row instruction fills LDS bytes [16 i, 16 i + 16), i.e. row i/8,
-  // physical chunk i%8, which must hold logical chunk (i%8) ^ (i/8).
-  const uint32_t lane_off = (uint32_t)((lane >> 3) * K + (((lane & 7) ^ (lane >> 3)) << 4));
+  // DMA: lane i of instruction J (stage rows 8J..8J+7) fills LDS bytes [16 i, 16 i + 16),
+  // i.e. row 8J + i/8, physical chunk i%8, which must hold logical chunk
+  // (i%8) ^ lds_swz(8J + i/8); that depends on the parity of J, hence two offsets.
+  uint32_t lane_off[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+    lane_off[par] = (uint32_t)((lane >> 3) * K + (((lane & 7) ^ lds_swz<GEMM_BK>(8 * par + (lane >> 3))) << 4));
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(w8 + (int64_t)n0 * K), 0, (int)((int64_t)(N - n0) * K), 0x00020000);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a8 + (int64_t)m0 * K), 0, (int)((int64_t)(M - m0) * K), 0x00020000);
   const int nk = (K + GEMM_BK - 1) / GEMM_BK;
-  const int tail_chunks = (K % GEMM_BK) >> 4;
-  constexpr int PER_STAGE = BN / 32 + BM / 32;
 
   v16f acc[TN][TM];
 #pragma unroll
@@ -146,57 +170,58 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_rowwise_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
-  const int wrow0 = wn * (BN / 2), xrow0 = wm * (BM / 2);
-  // Steady state: two stages per iteration, buffer 0 then buffer 1, while at least three
-  // stages remain; the last one or two stages (and the K tail) are peeled below so the
-  // loop body has no data-dependent control flow.
-  dma_tile<BN>(wrs, sW0, lane_off, K, wave, 0);
-  dma_tile<BM>(xrs, sX0, lane_off, K, wave, 0);
-  int ks = 0;
-  for (; ks + 2 < nk; ks += 2) {
-    dma_tile<BN>(wrs, sW1, lane_off, K, wave, (ks + 1) * GEMM_BK);
-    dma_tile<BM>(xrs, sX1, lane_off, K, wave, (ks + 1) * GEMM_BK);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_STAGE) : "memory");
+  const int wrow0 = wn * (C::BN / C::WN), xrow0 = wm * (C::BM / C::WM);
+  gemm_dma<C>(wrs, xrs, smem, lane_off, K, wave, 0);
+  for (int ks = 0; ks < nk; ++ks) {
+    uint8_t* cur = smem + (ks & 1) * C::STAGE;
+    // Stage ks is this wave's only DMA in flight.  After the barrier every wave's copy of
+    // stage ks has landed and every wave has finished stage ks-1, whose buffer then takes
+    // stage ks+1 while stage ks is multiplied.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     block_barrier();
-    mma_stage<TN, TM>(sW0, sX0, wrow0, xrow0, lane, acc);
-    block_barrier();
-    dma_tile<BN>(wrs, sW0, lane_off, K, wave, (ks + 2) * GEMM_BK);
-    dma_tile<BM>(xrs, sX0, lane_off, K, wave, (ks + 2) * GEMM_BK);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_STAGE) : "memory");
-    block_barrier();
-    mma_stage<TN, TM>(sW1, sX1, wrow0, xrow0, lane, acc);
-    block_barrier();
+    if (KTAIL && ks == nk - 1) {
+      zero_tail<C>(cur, (K % GEMM_BK) >> 4);
+      block_barrier();
+    }
+    if (ks + 1 < nk) gemm_dma<C>(wrs, xrs, smem + ((ks + 1) & 1) * C::STAGE, lane_off, K, wave, (ks + 1) * GEMM_BK);
+    mma_stage<C>(cur, wrow0, xrow0, lane, acc);
   }
-  // stage ks is in flight into buffer 0
-  const bool two_left = ks + 1 < nk;
-  if (two_left) {
-    dma_tile<BN>(wrs, sW1, lane_off, K, wave, (ks + 1) * GEMM_BK);
-    dma_tile<BM>(xrs, sX1, lane_off, K, wave, (ks + 1) * GEMM_BK);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_STAGE) : "memory");
-    block_barrier();
-    mma_stage<TN, TM>(sW0, sX0, wrow0, xrow0, lane, acc);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  block_barrier();
-  uint8_t* lW = two_left ? sW1 : sW0;
-  uint8_t* lX = two_left ? sX1 : sX0;
-  if (KTAIL) {
-    zero_tail<BN>(lW, tail_chunks);
-    zero_tail<BM>(lX, tail_chunks);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    block_barrier();
-  }
-  mma_stage<TN, TM>(lW, lX, wrow0, xrow0, lane, acc);
 
   // ---- epilogue ------------------------------------------------------------------------
+  // acc[a][b] register i: channel n = nb + 8 (i/4) + 4 g + i%4, token m = mb + lane%32.
   const int g = lane >> 5;
+  const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)bias) & 7) == 0) &&
+                      ((((uintptr_t)out) & 7) == 0);
 #pragma unroll
-  for (int b = 0; b < TM; ++b) {
-    const int m = m0 + wm * (BM / 2) + 32 * b + (lane & 31);
-    const float sam = sa[min(m, M - 1)];
+  for (int a = 0; a < TN; ++a) {
+    const int nb = n0 + wrow0 + 32 * a;
+    float swq[4][4], bq[4][4];
 #pragma unroll
-    for (int a = 0; a < TN; ++a) {
-      const int nb = n0 + wn * (BN / 2) + 32 * a;
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + 8 * q + 4 * g;
+      if (vec_ok && n + 3 < N) {
+        const v4f s4 = *reinterpret_cast<const v4f*>(sw + n);
+        swq[q][0] = s4[0]; swq[q][1] = s4[1]; swq[q][2] = s4[2]; swq[q][3] = s4[3];
+        if (bias) {
+          const uint2 b4 = *reinterpret_cast<const uint2*>(bias + n);
+          bq[q][0] = __uint_as_float(b4.x << 16); bq[q][1] = __uint_as_float(b4.x & 0xffff0000u);
+          bq[q][2] = __uint_as_float(b4.y << 16); bq[q][3] = __uint_as_float(b4.y & 0xffff0000u);
+        } else {
+          bq[q][0] = bq[q][1] = bq[q][2] = bq[q][3] = 0.0f;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int nn = min(n + e, N - 1);
+          swq[q][e] = sw[nn];
+          bq[q][e] = bias ? bf16_bits_to_f32(bias[nn]) : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < TM; ++b) {
+      const int m = m0 + xrow0 + 32 * b + (lane & 31);
+      const float sam = sa[min(m, M - 1)];
       v16f lacc;
       if constexpr (HAS_LORA) {
         // LoRA up-projection on the bf16 MFMA: lacc^T[n][m] = sum_j B[n][j] t[m][j]
@@ -217,9 +242,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_rowwise_kernel(
           uint32_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int nn = min(n + e, N - 1);
-            float v = acc[a][b][4 * q + e] * sam * sw[nn];
-            if (bias) v += bf16_bits_to_f32(bias[nn]);
+            float v = acc[a][b][4 * q + e] * sam * swq[q][e] + bq[q][e];
             v = bf16r(v);
             if constexpr (HAS_LORA) {
               const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
@@ -229,7 +252,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_rowwise_kernel(
             o[e] = f32_to_bf16_bits(v);
           }
           uint16_t* dst = out + (int64_t)m * ld_out + n;
-          if (n + 3 < N && ((ld_out & 3) == 0)) {
+          if (vec_ok && n + 3 < N) {
             *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
           } else {
 #pragma unroll
@@ -300,24 +323,24 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
     }
 }
 
-template <int BM, int BN, int ACT, bool LORA, bool KTAIL>
+template <class C, int ACT, bool LORA, bool KTAIL>
 static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
                         const uint16_t* bias, const uint16_t* lt, const uint16_t* lb, int r, float ls, uint16_t* out,
                         int M, int N, int K, int64_t ld_out, hipStream_t st) {
-  const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
-  gemm_fp8_rowwise_kernel<BM, BN, ACT, LORA, KTAIL><<<dim3(tiles_m * tiles_n), dim3(256), 0, st>>>(
+  const int tiles_m = (int)cdiv(M, C::BM), tiles_n = (int)cdiv(N, C::BN);
+  gemm_fp8_rowwise_kernel<C, ACT, LORA, KTAIL><<<dim3(tiles_m * tiles_n), dim3(C::THREADS), 0, st>>>(
       a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n);
 }
 
-template <int BM, int BN>
+template <class C>
 static void gemm_dispatch_tile(int act, bool lora, bool ktail, const uint8_t* a8, const uint8_t* w8,
                                const float* sa, const float* sw, const uint16_t* bias, const uint16_t* lt,
                                const uint16_t* lb, int r, float ls, uint16_t* out, int M, int N, int K,
                                int64_t ld_out, hipStream_t st) {
-#define MXF8_GEMM_CASE(A, L, T)                                                                  \
-  if (act == A && lora == L && ktail == T) {                                                     \
-    launch_gemm<BM, BN, A, L, T>(a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, st); \
-    return;                                                                                      \
+#define MXF8_GEMM_CASE(A, L, T)                                                                 \
+  if (act == A && lora == L && ktail == T) {                                                    \
+    launch_gemm<C, A, L, T>(a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, st); \
+    return;                                                                                     \
   }
   MXF8_GEMM_CASE(MXF8_ACT_NONE, false, false)
   MXF8_GEMM_CASE(MXF8_ACT_NONE, false, true)
@@ -365,10 +388,10 @@ extern "C" int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const flo
   // 256x256 tiles when they fill the chip, 128x128 otherwise.
   const int64_t big_tiles = cdiv(M, 256) * cdiv(N, 256);
   if (big_tiles >= 2 * 256)
-    gemm_dispatch_tile<256, 256>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
+    gemm_dispatch_tile<GemmBig>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
                                  ld_out, stream);
   else
-    gemm_dispatch_tile<128, 128>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
+    gemm_dispatch_tile<GemmSmall>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
                                  ld_out, stream);
   return check_launch("gemm_rowwise");
 }

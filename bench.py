@@ -39,6 +39,13 @@ if ROOT not in sys.path:
 METRIC = "FP8 GEMM + FP8 attn TFLOP/s (S=20k, D=128) and % of MI355X FP8 peak, 1 GPU"
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+# HBM bytes per launch of the attention kernel at S=20280, H=24, D=128, measured with
+# `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over this script's dispatches and
+# scaled by what the counters read for the 1 GiB streaming kernel of
+# hbm_stream_reference() (FETCH_SIZE reports 0.500 of the bytes read, WRITE_SIZE 1.000 of
+# the bytes written): 328108.7 KiB x 2 fetched + 122337.9 KiB written.  The algorithmic
+# traffic is 186.9 MB of Q8/K8/V8T read + 124.6 MB of output written.
+ATTN_TRAFFIC_BYTES = 328108.7 * 1024 * 2 + 122337.9 * 1024
 TOKENS = 20280                # 13 x 30 x 52
 HIDDEN, MLP = 3072, 12288
 HEADS, HEAD_DIM = 24, 128
@@ -135,6 +142,30 @@ def run_step(torch, ops, linears, qkv, timers: Timers | None):
     return outs
 
 
+def hbm_stream_reference(torch, dev, mib: int = 1024, reps: int = 5) -> dict:
+    """A plain streaming kernel of known traffic: y = -x over `mib` MiB of bf16.
+
+    Reports the HBM rate a simple elementwise kernel reaches on this device (read + write
+    bytes / kernel time), next to the quantizers' rates.  Under `rocprofv3 --pmc` its
+    dispatches are the calibration point of FETCH_SIZE / WRITE_SIZE (exactly `mib` MiB
+    read and written per launch).
+    """
+    n = mib * (1 << 20) // 2
+    x = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(x)
+    torch.neg(x, out=y)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        torch.neg(x, out=y)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    del x, y
+    return {"kernel": "torch.neg bf16 (elementwise)", "bytes_per_launch": 2 * mib * (1 << 20),
+            "ms": round(ms, 4), "GB/s": round(2 * mib * (1 << 20) / ms / 1e6, 1)}
+
+
 def cpu_baseline(target_s: float = 12.0) -> dict:
     """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix."""
     import torch
@@ -209,6 +240,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _native.load()
     _native.require_gfx950(dev)
+    log("[bench] HBM streaming reference")
+    stream_ref = hbm_stream_reference(torch, dev)
     log("[bench] building workload")
     linears, qkv = build_workload(torch, dev)
     torch.cuda.synchronize()
@@ -288,9 +321,10 @@ def main() -> int:
             "peak": PEAK_FP8_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
-            "traffic": None,
+            "traffic": round(ATTN_TRAFFIC_BYTES),
         },
         "kernels": parts,
+        "hbm_stream_reference": stream_ref,
     }
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline")

@@ -8,25 +8,27 @@
 // (0 below 8); l += sum(P); O += P V; with repair_tau >= 0, exp2(S - m) - P is added for
 // codes >= tau through bf16.  Output = O * sv / max(l, 1e-12).
 //
-// Mapping to CDNA4.  A workgroup (4 waves) owns one Q tile; wave w owns its 32 rows, and
-// two workgroups share a CU (the kernel is register-limited to 256 VGPRs per lane) so that
-// one wave's softmax (VALU) overlaps the other's matrix products on each SIMD.  The
-// kernel computes the TRANSPOSED score tile S^T = K Q^T with v_mfma_f32_32x32x64_f8f6f4:
-// in the 32x32 accumulator layout lane l holds query column l%32, so every per-query
-// statistic is lane-local (plus one exchange with lane l^32).  The K rows of each 32-key
-// subtile are fed to the MFMA in a permuted order chosen so that the accumulator
-// registers, packed 4 codes per dword, ARE the B operand of the PV MFMA (O^T = V^T P^T)
-// with V^T read as contiguous 32-byte runs of a v8t row: no cross-lane shuffles between
-// the two products.  The row sums l come from the matrix cores too: one more MFMA per
-// 64 keys with an all-ones A operand.  K and V^T tiles (and the mask / bias of the tile)
-// are copied global -> LDS by the direct-to-LDS DMA into two buffers; one barrier per
-// tile both publishes tile i and retires the buffer that tile i+1 is loaded into.
+// Mapping to CDNA4.  A workgroup of 4 waves owns one Q tile;
+// wave w owns its 32 rows.  The kernels compute the TRANSPOSED score tile S^T = K Q^T with
+// v_mfma_f32_32x32x64_f8f6f4: in the 32x32 accumulator layout lane l holds query column
+// l%32, so every per-query statistic is lane-local (plus one exchange with lane l^32).  The
+// K rows of each 32-key subtile are fed to the MFMA in a permuted order chosen so that the
+// accumulator registers, packed 4 codes per dword, ARE the B operand of the PV MFMA
+// (O^T = V^T P^T) with V^T read as contiguous 32-byte runs of a v8t row: no cross-lane
+// shuffles between the two products.  The row sums l come from the matrix cores too: one
+// more MFMA per 64 keys with an all-ones A operand.  K and V^T tiles (and the mask / bias
+// of the tile) are copied global -> LDS by the direct-to-LDS DMA.
 //
 // Per score the VALU does half a 3-input max, two FMAs (8 S + 56 - 8 m straight from the
 // fp32 dot product with the per-tile constant 8 sq sk, and the same shifted and scaled
 // for the flush test), a min and a rounding byte pack.  Folding sq * sk into one constant
 // rounds 8 S once instead of twice; the row max that drives the lazy-max policy is still
 // computed exactly as (max * sq) * sk.
+//
+// One workgroup per Q tile processes one KV tile at a time: S = QK^T, codes, PV (plus the
+// repair).  Two workgroups share a CU (without repair the kernel fits 256 VGPRs), so one
+// wave's softmax overlaps the other's matrix products on each SIMD.  Each run of matrix
+// products fetches its LDS fragments three products ahead.
 #pragma once
 
 #include "common.h"
@@ -54,93 +56,161 @@ struct AttnTile {
   static constexpr int VB = D * 128;             // V^T tile bytes (D rows x 128 keys)
   static constexpr int AUXB = AUX ? 2048 : 0;    // bias (1 KB) + mask (1 KB)
   static constexpr int BUF = KB + VB + AUXB;     // one LDS buffer
-  static constexpr int CPRK = D / 16;            // 16-byte chunks per K row
   static constexpr int K_INSTR = KB / 1024 / 4;  // 1 KB DMA instructions per wave
   static constexpr int V_INSTR = VB / 1024 / 4;
 };
 
-// 32 bytes = logical chunks chunk0, chunk0 + 1 of `row` of a swizzled tile.
-template <int ROW_BYTES>
-__device__ __forceinline__ v8i lds_read32(const uint8_t* tile, int row, int chunk0) {
-  const int sw = lds_swz<ROW_BYTES>(row);
-  const v4i lo = *reinterpret_cast<const v4i*>(tile + row * ROW_BYTES + ((chunk0 ^ sw) << 4));
-  const v4i hi = *reinterpret_cast<const v4i*>(tile + row * ROW_BYTES + (((chunk0 + 1) ^ sw) << 4));
-  v8i r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return r;
+// Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous range of
+// work items so that the workgroups resident on one XCD are consecutive Q tiles of one
+// head, whose staggered KV sweeps overlap and share that XCD's L2.
+__device__ __forceinline__ int xcd_linear_id(int L, int total) {
+  const int q = total >> 3, r = total & 7, x = L & 7, kk = L >> 3;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + kk;
 }
 
-// DMA one KV tile (keys [kv0, kv0 + 128)) of head bh into the LDS buffer `buf`.
+// Per-workgroup constants of a (b, h, Q tile) work item.
 template <int D, bool HAS_MASK, bool HAS_BIAS>
-__device__ __forceinline__ void attn_dma(__amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
-                                         __amdgpu_buffer_rsrc_t brs, __amdgpu_buffer_rsrc_t mrs, uint8_t* buf,
-                                         const uint32_t (&k_lane)[2], const uint32_t (&v_lane)[2], int wave, int lane,
-                                         int kv0, int Skp,
-                                         int Sk, const float* bias_row, const uint8_t* mask_row) {
-  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
-  uint8_t* sK = buf;
-  uint8_t* sV = buf + T::KB;
-  uint8_t* sAux = buf + T::KB + T::VB;
+struct AttnCtx {
+  int b, h, bh, I, nk, Skp, wave, lane, qrow;
+  float sqI;
+  const float* skh;
+  v8i qf[D / 64];
+  __amdgpu_buffer_rsrc_t krs, vrs, brs, mrs;
+  const float* brow;
+  const uint8_t* mrow;
+  uint32_t k_lane[2], v_lane[2];
+
+  // Work item id = bh * nq + I (head, Q tile); wave = the wave's index within the 4 waves
+  // that own the Q tile.
+  __device__ __forceinline__ AttnCtx(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t, const float* sq,
+                                     const float* sk, const uint8_t* key_mask, const float* key_bias, int H, int Sk,
+                                     int nq, int id, int wave_, int lane_) {
+    bh = id / nq;
+    I = id - bh * nq;
+    b = bh / H;
+    h = bh - b * H;
+    nk = (Sk + 127) / 128;
+    const int Sqp = nq * 128;
+    Skp = nk * 128;
+    wave = wave_;
+    lane = lane_;
+    const int g = lane >> 5;
+
+    // Q fragments (B operand of S^T): query row qrow, bytes [64 hh + 32 g, +32)
+    qrow = I * 128 + wave * 32 + (lane & 31);
+    const uint8_t* qp = q8 + ((int64_t)bh * Sqp + qrow) * D + 32 * g;
 #pragma unroll
-  for (int j = 0; j < T::K_INSTR; ++j) {
-    const int J = wave * T::K_INSTR + j;
-    // LDS rows of instruction J: accumulator row R of subtile t = R/32 loads key key_of_row.
-    int ubase;
-    if constexpr (D == 128) {
-      const int t = J >> 2;
-      ubase = 64 * (t >> 1) + 16 * (t & 1) + 4 * (J & 3);
-    } else {
-      const int t = J >> 1;
-      ubase = 64 * (t >> 1) + 16 * (t & 1) + 8 * (J & 1);
+    for (int hh = 0; hh < D / 64; ++hh) {
+      const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
+      const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
+      qf[hh][0] = lo[0]; qf[hh][1] = lo[1]; qf[hh][2] = lo[2]; qf[hh][3] = lo[3];
+      qf[hh][4] = hi[0]; qf[hh][5] = hi[1]; qf[hh][6] = hi[2]; qf[hh][7] = hi[3];
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, LDS_PTR(sK + J * 1024), 16, k_lane[j & 1], (kv0 + ubase) * D, 0,
-                                             0);
-  }
+    sqI = sq[(int64_t)bh * nq + I];
+    skh = sk + (int64_t)bh * nk;
+
+    krs = __builtin_amdgcn_make_buffer_rsrc((void*)(k8 + (int64_t)bh * Skp * D), 0, Skp * D, 0x00020000);
+    vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(v8t + (int64_t)bh * D * Skp), 0, D * Skp, 0x00020000);
+    brs = krs;
+    mrs = krs;
+    if constexpr (HAS_BIAS)
+      brs = __builtin_amdgcn_make_buffer_rsrc((void*)(key_bias + (int64_t)b * Sk), 0, Sk * 4, 0x00020000);
+    if constexpr (HAS_MASK)
+      mrs = __builtin_amdgcn_make_buffer_rsrc((void*)(key_mask + (int64_t)b * Sk), 0, Sk, 0x00020000);
+    brow = HAS_BIAS ? key_bias + (int64_t)b * Sk : nullptr;
+    mrow = HAS_MASK ? key_mask + (int64_t)b * Sk : nullptr;
+    // Per-lane DMA offsets.  A 1 KB DMA instruction J fills LDS bytes [1024 J, +1024): lane
+    // i writes 16 bytes at row 8J + i/8 (128-byte rows) or 16J + i/4 (64-byte rows),
+    // physical chunk i%8 (i%4), which must hold logical chunk phys ^ lds_swz(row); for
+    // 128-byte rows that depends on the parity of J, hence one offset per parity.
 #pragma unroll
-  for (int j = 0; j < T::V_INSTR; ++j) {
-    const int J = wave * T::V_INSTR + j;  // V^T rows [8J, 8J + 8)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, LDS_PTR(sV + J * 1024), 16, v_lane[j & 1], 8 * J * Skp + kv0, 0,
-                                             0);
-  }
-  // Mask / bias of the tile.  Full tiles use the DMA; the partial last tile loads element by
-  // element with a bounds check (a 16-byte DMA chunk that straddles the end of a [B, Sk]
-  // row is range-checked as a whole and would read back as zeros).
-  const bool tail = kv0 + 128 > Sk;
-  if constexpr (HAS_BIAS) {
-    if (wave == 0) {
-      if (!tail) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, LDS_PTR(sAux), 16, (uint32_t)(kv0 * 4 + (lane & 31) * 16), 0,
-                                                 0, 0);
-      } else if (lane < 32) {
-        v4f b4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = kv0 + 4 * lane + e;
-          b4[e] = key < Sk ? bias_row[key] : 0.0f;
-        }
-        *reinterpret_cast<v4f*>(sAux + 16 * lane) = b4;
+    for (int par = 0; par < 2; ++par) {
+      const int vrow = 8 * par + (lane >> 3);  // row of a 128-byte-row tile, mod 16
+      const uint32_t chunk128 = (uint32_t)(((lane & 7) ^ lds_swz<128>(vrow)) << 4);
+      v_lane[par] = (uint32_t)((lane >> 3) * Skp) + chunk128;
+      if constexpr (D == 128) {
+        // key of LDS row 8J + i/8 relative to the instruction's first key (key_of_row)
+        k_lane[par] = (uint32_t)((32 * ((lane >> 5) & 1) + ((lane >> 3) & 3)) * D) + chunk128;
+      } else {
+        const int rr = lane >> 2;  // row within the 16-row instruction, R = 16(J&1) + rr
+        k_lane[par] = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D +
+                                 (((lane & 3) ^ lds_swz<64>(rr)) << 4));
       }
     }
   }
-  if constexpr (HAS_MASK) {
-    if (wave == 1) {
-      if (!tail) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, LDS_PTR(sAux + 1024), 16, (uint32_t)(kv0 + (lane & 7) * 16), 0,
-                                                 0, 0);
-      } else if (lane < 8) {
-        uint32_t w[4] = {0, 0, 0, 0};
+
+  // Key tile (keys [kv0, kv0 + 128)) -> sK, rows permuted by key_of_row.
+  __device__ __forceinline__ void dma_k(uint8_t* sK, int kv0) const {
+    typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kv0 + 16 * lane + e;
-          const uint32_t byte = key < Sk ? (uint32_t)mask_row[key] : 0u;
-          w[e >> 2] |= byte << (8 * (e & 3));
+    for (int j = 0; j < T::K_INSTR; ++j) {
+      const int J = wave * T::K_INSTR + j;
+      // LDS rows of instruction J: accumulator row R of subtile t = R/32 loads key key_of_row.
+      int ubase;
+      if constexpr (D == 128) {
+        const int t = J >> 2;
+        ubase = 64 * (t >> 1) + 16 * (t & 1) + 4 * (J & 3);
+      } else {
+        const int t = J >> 1;
+        ubase = 64 * (t >> 1) + 16 * (t & 1) + 8 * (J & 1);
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, LDS_PTR(sK + J * 1024), 16, k_lane[j & 1], (kv0 + ubase) * D, 0,
+                                               0);
+    }
+  }
+
+  // V^T tile (D rows x keys [kv0, kv0 + 128)) -> sV.
+  __device__ __forceinline__ void dma_v(uint8_t* sV, int kv0) const {
+    typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+#pragma unroll
+    for (int j = 0; j < T::V_INSTR; ++j) {
+      const int J = wave * T::V_INSTR + j;  // V^T rows [8J, 8J + 8)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, LDS_PTR(sV + J * 1024), 16, v_lane[j & 1], 8 * J * Skp + kv0, 0,
+                                               0);
+    }
+  }
+
+  // Mask / bias of keys [kv0, kv0 + 128) -> sAux (bias fp32 at 0, mask bytes at 1024).  Full
+  // tiles use the DMA; the partial last tile loads element by element with a bounds check
+  // (a 16-byte DMA chunk that straddles the end of a [B, Sk] row is range-checked as a
+  // whole and would read back as zeros).
+  __device__ __forceinline__ void dma_aux(uint8_t* sAux, int kv0, int Sk) const {
+    const bool tail = kv0 + 128 > Sk;
+    if constexpr (HAS_BIAS) {
+      if (wave == 0) {
+        if (!tail) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, LDS_PTR(sAux), 16, (uint32_t)(kv0 * 4 + (lane & 31) * 16), 0,
+                                                   0, 0);
+        } else if (lane < 32) {
+          v4f b4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = kv0 + 4 * lane + e;
+            b4[e] = key < Sk ? brow[key] : 0.0f;
+          }
+          *reinterpret_cast<v4f*>(sAux + 16 * lane) = b4;
         }
-        *reinterpret_cast<v4i*>(sAux + 1024 + 16 * lane) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      }
+    }
+    if constexpr (HAS_MASK) {
+      if (wave == 1) {
+        if (!tail) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, LDS_PTR(sAux + 1024), 16, (uint32_t)(kv0 + (lane & 7) * 16),
+                                                   0, 0, 0);
+        } else if (lane < 8) {
+          uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kv0 + 16 * lane + e;
+            const uint32_t byte = key < Sk ? (uint32_t)mrow[key] : 0u;
+            w[e >> 2] |= byte << (8 * (e & 3));
+          }
+          *reinterpret_cast<v4i*>(sAux + 1024 + 16 * lane) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        }
       }
     }
   }
-}
+};
 
 template <int D, bool DO_REPAIR>
 struct AttnState {
@@ -150,6 +220,36 @@ struct AttnState {
   v16f lacc;     // every register holds the running sum of P codes of the lane's query
   float m;       // lazy row max (log2 domain)
   float ldelta;  // repair: running sum of the exact-minus-code corrections (lane's keys)
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o[dt][i] = 0.0f;
+        if constexpr (DO_REPAIR) orep[dt][i] = 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+    m = kAttnNeg;
+    ldelta = 0.0f;
+  }
+
+  // O, O_r, l *= alpha (a moved lazy max)
+  __device__ __forceinline__ void rescale(float alpha) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+      if constexpr (DO_REPAIR) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) orep[dt][i] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lacc[i] *= alpha;
+    if constexpr (DO_REPAIR) ldelta *= alpha;
+  }
 };
 
 // e4m3 value of a P code (codes are 0 or in [8, 126], i.e. zero or normal).
@@ -157,104 +257,173 @@ __device__ __forceinline__ float p_value(uint32_t code) {
   return code ? __uint_as_float((code << 20) + 0x3C000000u) : 0.0f;
 }
 
-// Process one KV tile held in LDS buffer `buf`.
-template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR>
-__device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D / 64], float sq, float skj, int kv0,
-                                          int Sk, float tau, int lane, AttnState<D, DO_REPAIR>& st) {
-  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
-  constexpr int NDT = D / 32;
-  constexpr float LOG2E_F = 1.4426950408889634f;
-  const uint8_t* sK = buf;
-  const uint8_t* sV = buf + T::KB;
-  const uint8_t* sAux = buf + T::KB + T::VB;
-  const int g = lane >> 5;
+// Lane offsets of the 16-byte LDS chunks a lane reads for its MFMA A fragments.  Row
+// 32x + r of a swizzled tile has the same swizzle as row r (lds_swz depends on row / 2 or
+// row / 4 modulo 8 / 4), so the subtile (t) and channel-tile (dt) offsets are immediates.
+template <int D>
+struct AttnFragOfs {
+  int k[D / 64][2];  // K tile: half hh, chunk 4 hh + 2 g + e
+  int v[2][2];       // V^T tile: key half kh, chunk 4 kh + 2 g + e
+  __device__ __forceinline__ explicit AttnFragOfs(int lane) {
+    const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) k[hh][e] = r * D + (((4 * hh + 2 * g + e) ^ lds_swz<D>(r)) << 4);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) v[kh][e] = r * 128 + (((4 * kh + 2 * g + e) ^ lds_swz<128>(r)) << 4);
+  }
+};
 
-  // ---- S^T = K Q^T (4 subtiles of 32 keys x 32 queries); s[t][i] is key 64(t/2) + 32g + 16(t%2) + i
-  v16f s[4];
+__device__ __forceinline__ v8i lds_pair(const uint8_t* base, int o0, int o1) {
+  const v4i lo = *reinterpret_cast<const v4i*>(base + o0);
+  const v4i hi = *reinterpret_cast<const v4i*>(base + o1);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+// A run of matrix-core products with their A fragments fetched from LDS three products
+// ahead (four fragments in flight), so the products issue back to back instead of each
+// waiting for its own LDS read.  The run is the PV products of one tile (when PV: O^T tile
+// x of key half kh, or the row-sum product when x == D/32) followed by the QK^T products
+// of another (when QK: subtile u, half hh).
+template <int D, bool PV, bool QK>
+struct AttnMfmaRun {
+  static constexpr int NDT = D / 32, QKM = D / 64;
+  static constexpr int NPV = PV ? 2 * (NDT + 1) : 0, NQK = QK ? 4 * QKM : 0, N = NPV + NQK;
+
+  template <int K>
+  __device__ static __forceinline__ v8i frag(const uint8_t* sV, const uint8_t* sK, const AttnFragOfs<D>& fo) {
+    if constexpr (K < NPV) {
+      constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
+      if constexpr (x == NDT)
+        return v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+      else
+        return lds_pair(sV + x * 32 * 128, fo.v[kh][0], fo.v[kh][1]);
+    } else {
+      constexpr int u = (K - NPV) / QKM, hh = (K - NPV) % QKM;
+      return lds_pair(sK + u * 32 * D, fo.k[hh][0], fo.k[hh][1]);
+    }
+  }
+
+  template <int K, bool REP>
+  __device__ static __forceinline__ void exec(const v8i& fr, const v8i (&pf)[2], const v8i (&qf)[D / 64],
+                                              v16f (&s)[4], AttnState<D, REP>& st) {
+    if constexpr (K < NPV) {
+      constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
+      if constexpr (x == NDT)
+        st.lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
+      else
+        st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pf[kh], st.o[x], 0, 0, 0, 0, 0, 0);
+    } else {
+      constexpr int u = (K - NPV) / QKM, hh = (K - NPV) % QKM;
+      if constexpr (hh == 0) {
+        v16f z;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+        s[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, qf[0], z, 0, 0, 0, 0, 0, 0);
+      } else {
+        s[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, qf[hh], s[u], 0, 0, 0, 0, 0, 0);
+      }
+    }
+  }
+
+  template <int K, bool REP>
+  __device__ static __forceinline__ void seq(v8i (&fr)[4], const uint8_t* sV, const uint8_t* sK,
+                                             const AttnFragOfs<D>& fo, const v8i (&pf)[2], const v8i (&qf)[D / 64],
+                                             v16f (&s)[4], AttnState<D, REP>& st) {
+    if constexpr (K < N) {
+      if constexpr (K + 3 < N) fr[(K + 3) & 3] = frag<K + 3>(sV, sK, fo);
+      exec<K, REP>(fr[K & 3], pf, qf, s, st);
+      seq<K + 1, REP>(fr, sV, sK, fo, pf, qf, s, st);
+    }
+  }
+
+  template <bool REP>
+  __device__ static __forceinline__ void run(const uint8_t* sV, const uint8_t* sK, const AttnFragOfs<D>& fo,
+                                             const v8i (&pf)[2], const v8i (&qf)[D / 64], v16f (&s)[4],
+                                             AttnState<D, REP>& st) {
+    v8i fr[4];
+    fr[0] = frag<0>(sV, sK, fo);
+    if constexpr (N > 1) fr[1] = frag<1>(sV, sK, fo);
+    if constexpr (N > 2) fr[2] = frag<2>(sV, sK, fo);
+    seq<0, REP>(fr, sV, sK, fo, pf, qf, s, st);
+  }
+};
+
+// Invalid keys (past Sk, masked, bias <= -1e8) get S = -inf; with a bias S is formed
+// explicitly as (dot * sq) * sk + bias * log2 e.
+template <bool HAS_MASK, bool HAS_BIAS>
+__device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sAux, int kv0, int Sk, float sq,
+                                                 float skj, int lane) {
+  constexpr float LOG2E_F = 1.4426950408889634f;
+  const int g = lane >> 5;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
+    const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
+    float bias[16];
+    if constexpr (HAS_BIAS) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[t][i] = 0.0f;
-#pragma unroll
-    for (int h = 0; h < D / 64; ++h) {
-      const v8i kf = lds_read32<D>(sK, 32 * t + (lane & 31), 4 * h + 2 * g);
-      s[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf[h], s[t], 0, 0, 0, 0, 0, 0);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const v4f b4 = *reinterpret_cast<const v4f*>(sAux + (kb + 4 * q4) * 4);
+        bias[4 * q4 + 0] = b4[0]; bias[4 * q4 + 1] = b4[1]; bias[4 * q4 + 2] = b4[2]; bias[4 * q4 + 3] = b4[3];
+      }
     }
-  }
-
-  // ---- scores of invalid keys become -inf; with a bias, S is formed explicitly
-  const bool partial = kv0 + 128 > Sk;
-  if (HAS_MASK || HAS_BIAS || partial) {
+    uint32_t mbytes[4] = {~0u, ~0u, ~0u, ~0u};
+    if constexpr (HAS_MASK) {
+      const v4i m4 = *reinterpret_cast<const v4i*>(sAux + 1024 + kb);
+      mbytes[0] = m4[0]; mbytes[1] = m4[1]; mbytes[2] = m4[2]; mbytes[3] = m4[3];
+    }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
-      float bias[16];
+    for (int i = 0; i < 16; ++i) {
+      bool ok = kv0 + kb + i < Sk;
+      float v = s[t][i];
       if constexpr (HAS_BIAS) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const v4f b4 = *reinterpret_cast<const v4f*>(sAux + (kb + 4 * q4) * 4);
-          bias[4 * q4 + 0] = b4[0]; bias[4 * q4 + 1] = b4[1]; bias[4 * q4 + 2] = b4[2]; bias[4 * q4 + 3] = b4[3];
-        }
+        ok = ok && (bias[i] > -1.0e8f);
+        v = (v * sq) * skj + bias[i] * LOG2E_F;
       }
-      uint32_t mbytes[4] = {~0u, ~0u, ~0u, ~0u};
-      if constexpr (HAS_MASK) {
-        const v4i m4 = *reinterpret_cast<const v4i*>(sAux + 1024 + kb);
-        mbytes[0] = m4[0]; mbytes[1] = m4[1]; mbytes[2] = m4[2]; mbytes[3] = m4[3];
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        bool ok = kv0 + kb + i < Sk;
-        float v = s[t][i];
-        if constexpr (HAS_BIAS) {
-          ok = ok && (bias[i] > -1.0e8f);
-          v = (v * sq) * skj + bias[i] * LOG2E_F;
-        }
-        if constexpr (HAS_MASK) ok = ok && (((mbytes[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0u);
-        s[t][i] = ok ? v : -INFINITY;
-      }
+      if constexpr (HAS_MASK) ok = ok && (((mbytes[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0u);
+      s[t][i] = ok ? v : -INFINITY;
     }
   }
+}
 
-  // ---- row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic)
-  float mx = -INFINITY;
+// Row max of the tile, the lazy-max decision and the exp2-free P codes.  Returns the new
+// row max m_new of the lane's query; pf receives the codes (the PV B operand).
+//
+// code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
+// 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
+// inactive.  v_cvt_pk_u8_f32 rounds to nearest even and saturates negative inputs to 0, so
+// it performs rint itself; the flush below 8 is min(bits, (bits - 8) * 2^24), negative
+// exactly when bits < 8 and equal to bits when bits >= 8 + 2^-21.  Invalid keys carry
+// S = -inf and flush to 0.
+template <bool HAS_BIAS>
+__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, v8i (&pf)[2]) {
+  // row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic), as four
+  // independent v_max3 chains so that the VALU need not wait on each result
+  float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float rmax = fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
-
-  // ---- lazy max
-  const float m_old = st.m;
-  const float m_new = (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
-  if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {  // wave-uniform: skip when no row moved
-    const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st.o[dt][i] *= alpha;
-      if constexpr (DO_REPAIR) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st.orep[dt][i] *= alpha;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) st.lacc[i] *= alpha;
-    if constexpr (DO_REPAIR) st.ldelta *= alpha;
+    for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], s[t][i]);
+  float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+  {
+    // partner lane^32 through v_permlane32_swap (two copies: each half receives the other)
+    const uint32_t u = __float_as_uint(mx);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   }
-  st.m = m_new;
+  const float rmax = fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
+  const float m_new = (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
 
-  // ---- exp2-free P codes: code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m.  bits
-  // never exceeds 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's
-  // clamp to [0, 126] is inactive.  v_cvt_pk_u8_f32 rounds to nearest even and saturates
-  // negative inputs to 0, so it performs rint itself; the flush below 8 is
-  // min(bits, (bits - 8) * 2^24), negative exactly when bits < 8 and equal to bits when
-  // bits >= 8 + 2^-21.  Invalid keys carry S = -inf and flush to 0.
   const float cst = 56.0f - 8.0f * m_new;
   const float c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
   const float c8f = c8 * 16777216.0f;
   const float cstf = (48.0f - 8.0f * m_new) * 16777216.0f;
-  v8i pf[2];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -266,189 +435,76 @@ __device__ __forceinline__ void attn_tile(const uint8_t* buf, const v8i (&qf)[D 
         const float flush = __builtin_fmaf(s[t][4 * w4 + e], c8f, cstf);
         word = __builtin_amdgcn_cvt_pk_u8_f32(fminf(bits, flush), e, word);
       }
+      // An empty use keeps the codes here instead of letting them sink to their consumer
+      // (the PV products, which the ping-pong kernel issues in another phase).
+      asm volatile("" ::"v"(word));
       pf[t >> 1][4 * (t & 1) + w4] = (int)word;
     }
   }
-
-  // ---- O^T += V^T P^T, l += 1^T P^T
-  const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
-#pragma unroll
-  for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const v8i vf = lds_read32<128>(sV, 32 * dt + (lane & 31), 4 * kh + 2 * g);
-      st.o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf[kh], st.o[dt], 0, 0, 0, 0, 0, 0);
-    }
-    st.lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
-  }
-
-  if constexpr (DO_REPAIR) {
-    // delta = exp2(S - m) - P where P >= tau; O_r^T += bf16(V^T) bf16(delta^T) over 16-key
-    // chunks: chunk (t, u) gives lane group g the 8 keys 64(t/2) + 16(t%2) + 32g + 8u + 0..7.
-    float dsum = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        v8bf db;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int i = 8 * u + e;
-          const uint32_t code = ((uint32_t)pf[t >> 1][4 * (t & 1) + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
-          const float papx = p_value(code);
-          const float S = HAS_BIAS ? s[t][i] : (s[t][i] * sq) * skj;
-          const float pexact = __builtin_amdgcn_exp2f(S - m_new);  // invalid keys: S = -inf -> 0
-          const float d = (papx >= tau) ? (pexact - papx) : 0.0f;
-          dsum += d;
-          db[e] = __builtin_bit_cast(__bf16, (unsigned short)f32_to_bf16_bits(d));
-        }
-        const int key0 = 64 * (t >> 1) + 16 * (t & 1) + 32 * g + 8 * u;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int row = 32 * dt + (lane & 31);
-          const int c = key0 >> 4;
-          const uint8_t* src = sV + row * 128 + ((c ^ lds_swz<128>(row)) << 4) + (key0 & 15);
-          const v2i raw = *reinterpret_cast<const v2i*>(src);
-          v8bf vb;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t byte = ((uint32_t)raw[e >> 2] >> (8 * (e & 3))) & 0xffu;
-            // e4m3 -> bf16 is exact: rebias the exponent (7 -> 127) and widen the mantissa.
-            const uint32_t sgn = (byte & 0x80u) << 8, mag = byte & 0x7fu;
-            uint32_t bits;
-            if (mag >= 8u) {
-              bits = sgn | ((mag + (120u << 3)) << 4);
-            } else {  // subnormal: mag * 2^-9
-              const float f = (float)mag * 0.001953125f;
-              bits = sgn | (__float_as_uint(f) >> 16);
-            }
-            vb[e] = __builtin_bit_cast(__bf16, (unsigned short)bits);
-          }
-          st.orep[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, db, st.orep[dt], 0, 0, 0);
-        }
-      }
-    }
-    st.ldelta += dsum;
-  }
+  return m_new;
 }
 
-// Register budget: 256 VGPRs per lane (two waves per SIMD) for the plain kernel; the
-// repair variant keeps S, codes and the correction accumulator live and runs one wave.
-template <bool DO_REPAIR>
-struct AttnOccupancy {
-  static constexpr int waves = DO_REPAIR ? 1 : 2;
-};
-
-template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOccupancy<DO_REPAIR>::waves)))
-void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
-                     const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
-                     const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
-                     void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H, int Sq,
-                     int Sk, int nq) {
-  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+// Repair: delta = exp2(S - m) - P where P >= tau; O_r^T += bf16(V^T) bf16(delta^T) over
+// 16-key chunks: chunk (t, u) gives lane group g the 8 keys 64(t/2) + 16(t%2) + 32g + 8u + 0..7.
+template <int D, bool HAS_BIAS>
+__device__ __forceinline__ void attn_repair(const uint8_t* sV, const v16f (&s)[4], const v8i (&pf)[2], float sq,
+                                            float skj, float m_new, float tau, int lane, AttnState<D, true>& st) {
   constexpr int NDT = D / 32;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * T::BUF];
-
-  // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous range of
-  // (head, Q tile) ids so that the workgroups resident on one XCD are consecutive Q tiles
-  // of one head, whose staggered KV sweeps overlap and share that XCD's L2.
-  int bh, I;
-  {
-    const int total = gridDim.x, L = blockIdx.x;
-    const int q = total >> 3, r = total & 7, x = L & 7, kk = L >> 3;
-    const int id = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + kk;
-    bh = id / nq;
-    I = id - bh * nq;
-  }
-  const int b = bh / H, h = bh - (bh / H) * H;
-  const int nk = (Sk + 127) / 128;
-  const int Sqp = nq * 128, Skp = nk * 128;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 5;
-
-  // ---- Q fragments (B operand of S^T): query row q0 + lane%32, bytes [64h + 32g, +32)
-  const int qrow = I * 128 + wave * 32 + (lane & 31);
-  v8i qf[D / 64];
-  {
-    const uint8_t* qp = q8 + ((int64_t)bh * Sqp + qrow) * D + 32 * g;
+  float dsum = 0.0f;
 #pragma unroll
-    for (int hh = 0; hh < D / 64; ++hh) {
-      const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
-      const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
-      qf[hh][0] = lo[0]; qf[hh][1] = lo[1]; qf[hh][2] = lo[2]; qf[hh][3] = lo[3];
-      qf[hh][4] = hi[0]; qf[hh][5] = hi[1]; qf[hh][6] = hi[2]; qf[hh][7] = hi[3];
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      v8bf db;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * u + e;
+        const uint32_t code = ((uint32_t)pf[t >> 1][4 * (t & 1) + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
+        const float papx = p_value(code);
+        const float S = HAS_BIAS ? s[t][i] : (s[t][i] * sq) * skj;
+        const float pexact = __builtin_amdgcn_exp2f(S - m_new);  // invalid keys: S = -inf -> 0
+        const float d = (papx >= tau) ? (pexact - papx) : 0.0f;
+        dsum += d;
+        db[e] = __builtin_bit_cast(__bf16, (unsigned short)f32_to_bf16_bits(d));
+      }
+      const int key0 = 64 * (t >> 1) + 16 * (t & 1) + 32 * g + 8 * u;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int row = 32 * dt + (lane & 31);
+        const int c = key0 >> 4;
+        const uint8_t* src = sV + row * 128 + ((c ^ lds_swz<128>(row)) << 4) + (key0 & 15);
+        const v2i raw = *reinterpret_cast<const v2i*>(src);
+        v8bf vb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t byte = ((uint32_t)raw[e >> 2] >> (8 * (e & 3))) & 0xffu;
+          // e4m3 -> bf16 is exact: rebias the exponent (7 -> 127) and widen the mantissa.
+          const uint32_t sgn = (byte & 0x80u) << 8, mag = byte & 0x7fu;
+          uint32_t bits;
+          if (mag >= 8u) {
+            bits = sgn | ((mag + (120u << 3)) << 4);
+          } else {  // subnormal: mag * 2^-9
+            const float f = (float)mag * 0.001953125f;
+            bits = sgn | (__float_as_uint(f) >> 16);
+          }
+          vb[e] = __builtin_bit_cast(__bf16, (unsigned short)bits);
+        }
+        st.orep[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, db, st.orep[dt], 0, 0, 0);
+      }
     }
   }
-  const float sqI = sq[(int64_t)bh * nq + I];
-  const float* skh = sk + (int64_t)bh * nk;
+  st.ldelta += dsum;
+}
 
-  // ---- DMA descriptors and per-lane offsets
-  const __amdgpu_buffer_rsrc_t krs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(k8 + (int64_t)bh * Skp * D), 0, Skp * D, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(v8t + (int64_t)bh * D * Skp), 0, D * Skp, 0x00020000);
-  __amdgpu_buffer_rsrc_t brs = krs, mrs = krs;
-  if constexpr (HAS_BIAS)
-    brs = __builtin_amdgcn_make_buffer_rsrc((void*)(key_bias + (int64_t)b * Sk), 0, Sk * 4, 0x00020000);
-  if constexpr (HAS_MASK)
-    mrs = __builtin_amdgcn_make_buffer_rsrc((void*)(key_mask + (int64_t)b * Sk), 0, Sk, 0x00020000);
-  const float* brow = HAS_BIAS ? key_bias + (int64_t)b * Sk : nullptr;
-  const uint8_t* mrow = HAS_MASK ? key_mask + (int64_t)b * Sk : nullptr;
-  // Per-lane DMA offsets.  A 1 KB DMA instruction J fills LDS bytes [1024 J, +1024): lane i
-  // writes 16 bytes at row 8J + i/8 (128-byte rows) or 16J + i/4 (64-byte rows), physical
-  // chunk i%8 (i%4), which must hold logical chunk phys ^ lds_swz(row); for 128-byte rows
-  // that depends on the parity of J, hence one offset per parity.
-  uint32_t k_lane[2], v_lane[2];
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int vrow = 8 * par + (lane >> 3);  // row of a 128-byte-row tile, mod 16
-    const uint32_t chunk128 = (uint32_t)(((lane & 7) ^ lds_swz<128>(vrow)) << 4);
-    v_lane[par] = (uint32_t)((lane >> 3) * Skp) + chunk128;
-    if constexpr (D == 128) {
-      // key of LDS row 8J + i/8 relative to the instruction's first key (key_of_row)
-      k_lane[par] = (uint32_t)((32 * ((lane >> 5) & 1) + ((lane >> 3) & 3)) * D) + chunk128;
-    } else {
-      const int rr = lane >> 2;  // row within the 16-row instruction, R = 16(J&1) + rr
-      k_lane[par] = (uint32_t)((32 * ((rr >> 2) & 1) + 4 * (rr >> 3) + (rr & 3)) * D +
-                               (((lane & 3) ^ lds_swz<64>(rr)) << 4));
-    }
-  }
-
-  AttnState<D, DO_REPAIR> st;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      st.o[dt][i] = 0.0f;
-      if constexpr (DO_REPAIR) st.orep[dt][i] = 0.0f;
-    }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) st.lacc[i] = 0.0f;
-  st.m = kAttnNeg;
-  st.ldelta = 0.0f;
-
-  const int j0 = (int)(((int64_t)I * nk) / nq);
-  attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, smem, k_lane, v_lane, wave, lane, j0 * 128, Skp, Sk, brow,
-                                  mrow);
-  int j = j0;
-  for (int i = 0; i < nk; ++i) {
-    // Tile i is the only DMA in flight; after the barrier every wave has finished tile
-    // i-1, so its buffer can take tile i+1 while tile i is computed.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    attn_barrier();
-    const int jn = j + 1 == nk ? 0 : j + 1;
-    if (i + 1 < nk)
-      attn_dma<D, HAS_MASK, HAS_BIAS>(krs, vrs, brs, mrs, smem + ((i + 1) & 1) * T::BUF, k_lane, v_lane, wave, lane,
-                                      jn * 128, Skp, Sk, brow, mrow);
-    attn_tile<D, HAS_MASK, HAS_BIAS, DO_REPAIR>(smem + (i & 1) * T::BUF, qf, sqI, skh[j], j * 128, Sk, tau, lane,
-                                                st);
-    j = jn;
-  }
-
-  // ---- epilogue: O = (O + O_r) * sv / max(l, 1e-12); lane holds query qrow, channels
-  // 32 dt + 8 (i/4) + 4 g + i%4
-  if (qrow >= Sq) return;
+// O = (O + O_r) * sv / max(l, 1e-12) -> out (bf16 / fp16 through its strides).  The lane
+// holds query qrow, channels 32 dt + 8 (i/4) + 4 g + i%4.
+template <int D, bool DO_REPAIR, int ODT>
+__device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, const float* sv, int bh, int b, int h,
+                                           int qrow, int lane, void* out, int64_t os_b, int64_t os_h, int64_t os_s,
+                                           int64_t os_d) {
+  constexpr int NDT = D / 32;
+  const int g = lane >> 5;
   float l = st.lacc[0];
   if constexpr (DO_REPAIR) l += st.ldelta + __shfl_xor(st.ldelta, 32, 64);
   const float den = fmaxf(l, 1.0e-12f);
@@ -477,6 +533,69 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// One tile at a time: per KV tile, S = QK^T, codes, PV (and the repair).  Without repair
+// two waves per SIMD fit (256 VGPRs); the repair keeps more live and runs one.
+// ---------------------------------------------------------------------------------------
+template <bool DO_REPAIR>
+struct AttnOccupancy {
+  static constexpr int waves = DO_REPAIR ? 1 : 2;
+};
+
+template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOccupancy<DO_REPAIR>::waves)))
+void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
+                     const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
+                     const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
+                     void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H, int Sq,
+                     int Sk, int nq) {
+  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * T::BUF];
+  const AttnCtx<D, HAS_MASK, HAS_BIAS> cx(q8, k8, v8t, sq, sk, key_mask, key_bias, H, Sk, nq,
+                                          xcd_linear_id(blockIdx.x, gridDim.x),
+                                          __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
+  const int nk = cx.nk, lane = cx.lane;
+  const AttnFragOfs<D> fo(lane);
+
+  AttnState<D, DO_REPAIR> st;
+  st.init();
+
+  const int j0 = (int)(((int64_t)cx.I * nk) / nq);
+  cx.dma_k(smem, j0 * 128);
+  cx.dma_v(smem + T::KB, j0 * 128);
+  cx.dma_aux(smem + T::KB + T::VB, j0 * 128, Sk);
+  int j = j0;
+  for (int i = 0; i < nk; ++i) {
+    // Tile i is the only DMA in flight; after the barrier every wave has finished tile
+    // i-1, so its buffer can take tile i+1 while tile i is computed.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    attn_barrier();
+    const int jn = j + 1 == nk ? 0 : j + 1;
+    if (i + 1 < nk) {
+      uint8_t* nb = smem + ((i + 1) & 1) * T::BUF;
+      cx.dma_k(nb, jn * 128);
+      cx.dma_v(nb + T::KB, jn * 128);
+      cx.dma_aux(nb + T::KB + T::VB, jn * 128, Sk);
+    }
+    const uint8_t* buf = smem + (i & 1) * T::BUF;
+    const float skj = cx.skh[j];
+    const int kv0 = j * 128;
+    v16f s[4];
+    v8i pf[2];
+    AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+    if (HAS_MASK || HAS_BIAS || kv0 + 128 > Sk)
+      attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
+    const float m_new = attn_codes<HAS_BIAS>(s, cx.sqI, skj, st.m, pf);
+    if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
+    st.m = m_new;
+    AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+    if constexpr (DO_REPAIR) attn_repair<D, HAS_BIAS>(buf + T::KB, s, pf, cx.sqI, skj, m_new, tau, lane, st);
+    j = jn;
+  }
+  if (cx.qrow >= Sq) return;
+  attn_store<D, DO_REPAIR, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
 }
 
 template <int D, bool M_, bool B_, bool R_, int ODT>

@@ -261,27 +261,57 @@ __global__ __launch_bounds__(256) void attn_colreduce_kernel(const void* __restr
   }
 }
 
-// mean[bh][d] = (sum over chunks, in order) / S
-template <int D>
-__global__ void attn_kmean_finalize_kernel(const float* __restrict__ part, int nch, int64_t S,
-                                           float* __restrict__ mean) {
+// Fold of the per-chunk slabs part[bh][chunk][d]: SUM -> out = sum / S (the key mean),
+// ABSMAX -> out = max(amax, 1e-12) / 448 (the per-channel V scale).  One block per (b, h):
+// 256 / D threads per channel each fold a contiguous quarter / half of the chunks with
+// eight independent partial results (loads in flight together), then the parts are
+// combined in a fixed order, so the result does not depend on scheduling.
+template <int D, bool ABSMAX>
+__global__ __launch_bounds__(256) void attn_colfold_kernel(const float* __restrict__ part, int nch, int64_t S,
+                                                           float* __restrict__ out) {
+  constexpr int PARTS = 256 / D;
+  __shared__ float red[PARTS][D];
   const int64_t bh = blockIdx.x;
-  const int d = threadIdx.x;
-  if (d >= D) return;
-  float a = 0.0f;
-  for (int c = 0; c < nch; ++c) a += part[(bh * nch + c) * D + d];
-  mean[bh * D + d] = __fdiv_rn(a, (float)S);
+  const int d = threadIdx.x % D, p = threadIdx.x / D;
+  const int c0 = p * nch / PARTS, c1 = (p + 1) * nch / PARTS;
+  const float* src = part + (bh * nch) * D + d;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = src[(int64_t)(c + i) * D];
+      acc[i] = ABSMAX ? fmaxf(acc[i], v) : acc[i] + v;
+    }
+  }
+  for (; c < c1; ++c) {
+    const float v = src[(int64_t)c * D];
+    acc[0] = ABSMAX ? fmaxf(acc[0], v) : acc[0] + v;
+  }
+#pragma unroll
+  for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) acc[i] = ABSMAX ? fmaxf(acc[i], acc[i + w]) : acc[i] + acc[i + w];
+  red[p][d] = acc[0];
+  __syncthreads();
+  if (p == 0) {
+    float a = red[0][d];
+#pragma unroll
+    for (int j = 1; j < PARTS; ++j) a = ABSMAX ? fmaxf(a, red[j][d]) : a + red[j][d];
+    out[bh * D + d] = ABSMAX ? e4m3_scale(a) : __fdiv_rn(a, (float)S);
+  }
 }
 
-// V quantizer, transposed store.  grid (Skp/128, B*H).  Each block folds the per-chunk
-// absmax slabs into sv (fixed order; max is exact), quantizes a 128-key x D tile and
-// writes it transposed through LDS so that every v8t row segment is a full 128 bytes.
+// V quantizer, transposed store.  grid (Skp/128, B*H).  Each block quantizes a 128-key x
+// D tile with the per-channel scales sv (from attn_colfold_kernel) and writes it transposed
+// through LDS so that every v8t row segment is a full 128 bytes.
 // Thread t handles d-chunk (t % CPR) of the 4 consecutive keys 4 * (t / CPR + KQP * p) + 0..3.
 template <int DT, int D, bool VEC>
 __global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
-                                                           int64_t S, int64_t Sp, const float* __restrict__ part,
-                                                           int nch, uint8_t* __restrict__ v8t,
-                                                           float* __restrict__ sv) {
+                                                           int64_t S, int64_t Sp, const float* __restrict__ sv,
+                                                           uint8_t* __restrict__ v8t) {
   constexpr int CPR = D / 8;
   constexpr int KQP = 256 / CPR;  // key quads per pass
   constexpr int NP = 32 / KQP;    // passes over the 32 key quads of the tile
@@ -293,12 +323,9 @@ __global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restric
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / H, h = bh % H;
   if (threadIdx.x < D) {
-    float a = 0.0f;
-    for (int c = 0; c < nch; ++c) a = fmaxf(a, part[(bh * nch + c) * D + threadIdx.x]);
-    const float s = e4m3_scale(a);
+    const float s = sv[bh * D + threadIdx.x];
     s_sv[threadIdx.x] = s;
     s_r[threadIdx.x] = __fdiv_rn(1.0f, s);
-    if (blk == 0) sv[bh * D + threadIdx.x] = s;
   }
   __syncthreads();
   const void* base = static_cast<const char*>(src) + (b * st.b + h * st.h) * (int64_t)sizeof(typename Elem<DT>::T);
@@ -479,21 +506,21 @@ extern "C" int mxf8_attn_kmean(const void* k, int dtype, const int64_t strides[4
   rc = check_launch("attn_kmean(partial)");
   if (rc) return rc;
   if (D == 128)
-    attn_kmean_finalize_kernel<128><<<dim3((unsigned)BH), dim3(128), 0, stream>>>(part, nch, S, mean);
+    attn_colfold_kernel<128, false><<<dim3((unsigned)BH), dim3(256), 0, stream>>>(part, nch, S, mean);
   else
-    attn_kmean_finalize_kernel<64><<<dim3((unsigned)BH), dim3(64), 0, stream>>>(part, nch, S, mean);
-  return check_launch("attn_kmean(finalize)");
+    attn_colfold_kernel<64, false><<<dim3((unsigned)BH), dim3(256), 0, stream>>>(part, nch, S, mean);
+  return check_launch("attn_kmean(fold)");
 }
 
 template <int DT, int D>
 static void launch_quant_v(const void* v, const Strides4& st, bool vec, int64_t H, int64_t S, int64_t BH,
-                           const float* part, int nch, uint8_t* v8t, float* sv, hipStream_t stream) {
+                           const float* sv, uint8_t* v8t, hipStream_t stream) {
   const int64_t nb = cdiv(S, 128);
   dim3 grid((unsigned)nb, (unsigned)BH);
   if (vec)
-    attn_quant_v_kernel<DT, D, true><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, part, nch, v8t, sv);
+    attn_quant_v_kernel<DT, D, true><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, sv, v8t);
   else
-    attn_quant_v_kernel<DT, D, false><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, part, nch, v8t, sv);
+    attn_quant_v_kernel<DT, D, false><<<grid, 256, 0, stream>>>(v, st, H, S, nb * 128, sv, v8t);
 }
 
 extern "C" int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides[4], int64_t B, int64_t H,
@@ -510,12 +537,18 @@ extern "C" int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides
   colreduce<true>(v, dtype, st, vec, H, S, D, BH, nch, part, stream);
   rc = check_launch("attn_quant_v(absmax)");
   if (rc) return rc;
+  if (D == 128)
+    attn_colfold_kernel<128, true><<<dim3((unsigned)BH), dim3(256), 0, stream>>>(part, nch, S, sv);
+  else
+    attn_colfold_kernel<64, true><<<dim3((unsigned)BH), dim3(256), 0, stream>>>(part, nch, S, sv);
+  rc = check_launch("attn_quant_v(scale)");
+  if (rc) return rc;
   if (dtype == MXF8_BF16) {
-    if (D == 128) launch_quant_v<MXF8_BF16, 128>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
-    else launch_quant_v<MXF8_BF16, 64>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+    if (D == 128) launch_quant_v<MXF8_BF16, 128>(v, st, vec, H, S, BH, sv, v8t, stream);
+    else launch_quant_v<MXF8_BF16, 64>(v, st, vec, H, S, BH, sv, v8t, stream);
   } else {
-    if (D == 128) launch_quant_v<MXF8_F16, 128>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
-    else launch_quant_v<MXF8_F16, 64>(v, st, vec, H, S, BH, part, nch, v8t, sv, stream);
+    if (D == 128) launch_quant_v<MXF8_F16, 128>(v, st, vec, H, S, BH, sv, v8t, stream);
+    else launch_quant_v<MXF8_F16, 64>(v, st, vec, H, S, BH, sv, v8t, stream);
   }
   return check_launch("attn_quant_v");
 }

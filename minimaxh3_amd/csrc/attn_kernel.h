@@ -19,11 +19,12 @@
 // more MFMA per 64 keys with an all-ones A operand.  K and V^T tiles (and the mask / bias
 // of the tile) are copied global -> LDS by the direct-to-LDS DMA.
 //
-// Per score the VALU does half a 3-input max, two FMAs (8 S + 56 - 8 m straight from the
-// fp32 dot product with the per-tile constant 8 sq sk, and the same shifted and scaled
-// for the flush test), a min and a rounding byte pack.  Folding sq * sk into one constant
-// rounds 8 S once instead of twice; the row max that drives the lazy-max policy is still
-// computed exactly as (max * sq) * sk.
+// Per score the VALU does half a 3-input max and three FMAs (8 S + 56 - 8 m straight from
+// the fp32 dot product with the per-tile constant 8 sq sk; the flush test as a clamped FMA;
+// rounding to an integer code by adding 1.5 * 2^23), plus three quarters of a byte
+// permute to pack the codes.  Folding sq * sk into one constant rounds 8 S once instead of
+// twice; the row max that drives the lazy-max policy is still computed exactly as
+// (max * sq) * sk.
 //
 // One workgroup per Q tile processes one KV tile at a time: S = QK^T, codes, PV (plus the
 // repair).  Two workgroups share a CU (without repair the kernel fits 256 VGPRs), so one
@@ -291,8 +292,9 @@ __device__ __forceinline__ v8i lds_pair(const uint8_t* base, int o0, int o1) {
 // waiting for its own LDS read.  The run is the PV products of one tile (when PV: O^T tile
 // x of key half kh, or the row-sum product when x == D/32) followed by the QK^T products
 // of another (when QK: subtile u, half hh).
-template <int D, bool PV, bool QK>
+template <int D, bool PV, bool QK, int AHEAD = 3>
 struct AttnMfmaRun {
+  static constexpr int RING = AHEAD + 1;
   static constexpr int NDT = D / 32, QKM = D / 64;
   static constexpr int NPV = PV ? 2 * (NDT + 1) : 0, NQK = QK ? 4 * QKM : 0, N = NPV + NQK;
 
@@ -339,6 +341,9 @@ struct AttnMfmaRun {
     if constexpr (K < N) {
       if constexpr (K + 3 < N) fr[(K + 3) & 3] = frag<K + 3>(sV, sK, fo);
       exec<K, REP>(fr[K & 3], pf, qf, s, st);
+      // keep program order: a reordered run would hold the scores and the PV fragments
+      // live together
+      __builtin_amdgcn_sched_barrier(0);
       seq<K + 1, REP>(fr, sV, sK, fo, pf, qf, s, st);
     }
   }
@@ -355,13 +360,24 @@ struct AttnMfmaRun {
   }
 };
 
-// Invalid keys (past Sk, masked, bias <= -1e8) get S = -inf; with a bias S is formed
-// explicitly as (dot * sq) * sk + bias * log2 e.
+// Score given to invalid keys: finite and so negative that it loses every row max and
+// flushes to code 0.  The code arithmetic multiplies it by c8 = 8 sq sk (or 8 with a bias),
+// so it is chosen to make that product -1e30 (finite: no inf * 0 = NaN downstream); for
+// c8 < 1e-8 it is -1e38 and the product is smaller still.
+template <bool HAS_BIAS>
+__device__ __forceinline__ float attn_invalid_score(float sq, float skj) {
+  if constexpr (HAS_BIAS) return -1.25e29f;
+  return -1.0e30f / fmaxf((8.0f * sq) * skj, 1.0e-8f);
+}
+
+// Invalid keys (past Sk, masked, bias <= -1e8) get attn_invalid_score; with a bias S is
+// formed explicitly as (dot * sq) * sk + bias * log2 e.
 template <bool HAS_MASK, bool HAS_BIAS>
 __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sAux, int kv0, int Sk, float sq,
                                                  float skj, int lane) {
   constexpr float LOG2E_F = 1.4426950408889634f;
   const int g = lane >> 5;
+  const float vinv = attn_invalid_score<HAS_BIAS>(sq, skj);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
@@ -387,7 +403,7 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
         v = (v * sq) * skj + bias[i] * LOG2E_F;
       }
       if constexpr (HAS_MASK) ok = ok && (((mbytes[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0u);
-      s[t][i] = ok ? v : -INFINITY;
+      s[t][i] = ok ? v : vinv;
     }
   }
 }
@@ -397,10 +413,15 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
 //
 // code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
 // 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
-// inactive.  v_cvt_pk_u8_f32 rounds to nearest even and saturates negative inputs to 0, so
-// it performs rint itself; the flush below 8 is min(bits, (bits - 8) * 2^24), negative
-// exactly when bits < 8 and equal to bits when bits >= 8 + 2^-21.  Invalid keys carry
-// S = -inf and flush to 0.
+// inactive.  Three FMAs per score, all at the full FMA rate:
+//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
+//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
+//   t    = fma(bits, keep, 1.5 * 2^23)
+// keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
+// is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
+// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
+// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
+// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
 template <bool HAS_BIAS>
 __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, v8i (&pf)[2]) {
   // row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic), as four
@@ -422,19 +443,23 @@ __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float 
 
   const float cst = 56.0f - 8.0f * m_new;
   const float c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
-  const float c8f = c8 * 16777216.0f;
-  const float cstf = (48.0f - 8.0f * m_new) * 16777216.0f;
+  const float c8f = c8 * 0x1p64f;
+  const float cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4) {
-      uint32_t word = 0;
+      uint32_t tb[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float bits = __builtin_fmaf(s[t][4 * w4 + e], c8, cst);
-        const float flush = __builtin_fmaf(s[t][4 * w4 + e], c8f, cstf);
-        word = __builtin_amdgcn_cvt_pk_u8_f32(fminf(bits, flush), e, word);
+        const float x = s[t][4 * w4 + e];
+        const float bits = __builtin_fmaf(x, c8, cst);
+        const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, c8f, cstf), 0.0f, 1.0f);
+        tb[e] = __float_as_uint(__builtin_fmaf(bits, keep, 12582912.0f));
       }
+      // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
+      const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
+                            __builtin_amdgcn_perm(tb[3], tb[2], 0x04000c0cu);
       // An empty use keeps the codes here instead of letting them sink to their consumer
       // (the PV products, which the ping-pong kernel issues in another phase).
       asm volatile("" ::"v"(word));
@@ -603,9 +628,8 @@ static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t
                         const float* sv, const uint8_t* km, const float* kb, float tau, void* out,
                         const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, hipStream_t st) {
   const int64_t nq = cdiv(Sq, 128);
-  dim3 grid((unsigned)(nq * B * H));
-  attn_fwd_kernel<D, M_, B_, R_, ODT><<<grid, 256, 0, st>>>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1],
-                                                            os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq);
+  attn_fwd_kernel<D, M_, B_, R_, ODT><<<dim3((unsigned)(nq * B * H)), 256, 0, st>>>(
+      q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq);
 }
 
 template <int D, int ODT>

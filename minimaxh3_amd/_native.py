@@ -52,7 +52,10 @@ def lib_path() -> str:
 
 
 def load(path: str | None = None):
-    """Load libmxf8.so (idempotent) and attach the argument types of every export."""
+    """Load libmxf8.so (idempotent) and attach the argument types of every export.
+
+    With `path`, that library is loaded and becomes the one every later load() returns.
+    """
     global _lib
     with _lock:
         if _lib is not None and path is None:
@@ -66,8 +69,8 @@ def load(path: str | None = None):
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if path is None:
-            _lib = lib
+        # an explicit path replaces the process-wide library: every later load() returns it
+        _lib = lib
         return lib
 
 

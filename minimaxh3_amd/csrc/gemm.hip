@@ -9,14 +9,19 @@
 //
 // Block tile BM (tokens) x BN (channels) x 128 (K stage) on WM x WN waves, each wave
 // (BM/WM) x (BN/WN) built from v_mfma_f32_32x32x64_f8f6f4.  The large configuration runs
-// 8 waves on a 256 x 256 tile, two waves per SIMD, so that one wave's LDS reads and
-// barrier waits overlap the other's matrix products.  Operand tiles are copied
-// global -> LDS with the direct-to-LDS DMA (buffer_load_dwordx4 ... lds: 64 lanes x 16
-// bytes into 1 KB of LDS) into two stage buffers; one barrier per stage publishes stage
-// k and retires the buffer that stage k+1 is then loaded into, so the copy of stage k+1
-// overlaps the MFMAs of stage k.  Inside a tile each 128-byte row holds 8 chunks of 16
-// bytes stored at chunk ^ lds_swz(row), which makes the ds_read_b128 fragment reads
-// bank-conflict free.
+// 8 waves on a 256 x 256 tile, two waves per SIMD.  Operand tiles are copied global -> LDS
+// with the direct-to-LDS DMA (buffer_load_dwordx4 ... lds: 64 lanes x 16 bytes = 8 rows x
+// 128 bytes, whole cache lines) into two stage buffers; one barrier per stage publishes
+// stage k and retires the buffer that stage k+1 is then loaded into.  Inside a stage the
+// fragments of the second 64-byte K half are read while the first half's products run.
+// Each 128-byte row holds 8 chunks of 16 bytes stored at chunk ^ lds_swz(row), which
+// makes the ds_read_b128 fragment reads bank-conflict free.
+//
+// The kernel is persistent: one workgroup per CU walks a sequence of output tiles.  The
+// first stage of the next tile is copied while the current tile's epilogue runs, and the
+// epilogue's channel scales, bias and token scales come from LDS (read into registers at
+// the start of the tile), so neither the pipeline fill nor a workgroup launch separates
+// two tiles.
 #include "common.h"
 
 namespace mxf8 {
@@ -56,15 +61,24 @@ __device__ __forceinline__ float gelu_tanh_f32(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-__device__ __forceinline__ float bf16r(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
-// Map the launch index to an output tile: first give every XCD a contiguous range of
-// tile ids (workgroups are dealt to the 8 XCDs round-robin), then walk that range in
-// groups of GROUP_M token-tiles so concurrently running tiles share operand panels in L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+// fp32 -> bf16 -> fp32 and fp32 pair -> packed bf16 pair, both with the hardware
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
+__device__ __forceinline__ uint32_t bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
+}
+
+// Map a tile sequence number s to an output tile.  Workgroups are dealt to the 8 XCDs
+// round-robin and a persistent workgroup b walks s = b, b + G, b + 2G, ... (G = grid, a
+// multiple of 8), so s % 8 names the XCD: give every XCD a contiguous range of tile ids,
+// then walk that range in groups of GROUP_M token-tiles so concurrently running tiles
+// share operand panels in the XCD's L2.
+__device__ __forceinline__ void tile_coords(int s, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int nwg = tiles_m * tiles_n;
-  const int i = blockIdx.x;
-  const int q = nwg >> 3, rem = nwg & 7, x = i & 7, j = i >> 3;
+  const int q = nwg >> 3, rem = nwg & 7, x = s & 7, j = s >> 3;
   const int id = (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + j;
   constexpr int GROUP_M = 8;
   const int per_group = GROUP_M * tiles_n;
@@ -118,20 +132,29 @@ __device__ __forceinline__ void mma_stage(const uint8_t* stage, int wrow0, int x
                                           v16f (&acc)[C::TN][C::TM]) {
   const uint8_t* tW = stage;
   const uint8_t* tX = stage + C::BN * GEMM_BK;
+  const int r = lane & 31, c0 = 2 * (lane >> 5), c1 = 4 + c0;
+  v8i af[C::TN], bf[C::TM], bf1[C::TM];
 #pragma unroll
-  for (int kh = 0; kh < 2; ++kh) {
-    const int c0 = 4 * kh + 2 * (lane >> 5);
-    v8i af[C::TN], bf[C::TM];
+  for (int t = 0; t < C::TN; ++t) af[t] = lds_frag(tW, wrow0 + 32 * t + r, c0);
 #pragma unroll
-    for (int t = 0; t < C::TN; ++t) af[t] = lds_frag(tW, wrow0 + 32 * t + (lane & 31), c0);
+  for (int t = 0; t < C::TM; ++t) bf[t] = lds_frag(tX, xrow0 + 32 * t + r, c0);
 #pragma unroll
-    for (int t = 0; t < C::TM; ++t) bf[t] = lds_frag(tX, xrow0 + 32 * t + (lane & 31), c0);
+  for (int t = 0; t < C::TM; ++t) bf1[t] = lds_frag(tX, xrow0 + 32 * t + r, c1);
+  // first K half; each A fragment's registers take its second-half fragment once its
+  // products have issued
 #pragma unroll
-    for (int a = 0; a < C::TN; ++a)
+  for (int a = 0; a < C::TN; ++a) {
 #pragma unroll
-      for (int b = 0; b < C::TM; ++b)
-        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+    for (int b = 0; b < C::TM; ++b)
+      acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+    af[a] = lds_frag(tW, wrow0 + 32 * a + r, c1);
+    __builtin_amdgcn_sched_barrier(0);
   }
+#pragma unroll
+  for (int a = 0; a < C::TN; ++a)
+#pragma unroll
+    for (int b = 0; b < C::TM; ++b)
+      acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf1[b], acc[a][b], 0, 0, 0, 0, 0, 0);
 }
 
 template <class C, int ACT, bool HAS_LORA, bool KTAIL>
@@ -141,14 +164,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const uint16_t* __restrict__ lora_b, int lora_r, float lora_scale, uint16_t* __restrict__ out, int M, int N,
     int K, int64_t ld_out, int tiles_m, int tiles_n) {
   constexpr int TM = C::TM, TN = C::TN;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+  constexpr int EP_BYTES = (2 * C::BN + C::BM) * 4;  // channel scales, bias (fp32), token scales
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + EP_BYTES];
+  static_assert(2 * C::STAGE + EP_BYTES <= 160 * 1024, "LDS exceeds the 160 KB of a CU");
+  float* const ep_sw = reinterpret_cast<float*>(smem + 2 * C::STAGE);  // [BN]
+  float* const ep_b = ep_sw + C::BN;                                   // [BN]
+  float* const ep_sa = ep_b + C::BN;                                   // [BM]
 
-  int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  const int ntiles = tiles_m * tiles_n;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wn = wave / C::WM, wm = wave % C::WM;
-
+  const int wrow0 = wn * (C::BN / C::WN), xrow0 = wm * (C::BM / C::WM);
+  const int nk = (K + GEMM_BK - 1) / GEMM_BK;
   // DMA: lane i of instruction J (stage rows 8J..8J+7) fills LDS bytes [16 i, 16 i + 16),
   // i.e. row 8J + i/8, physical chunk i%8, which must hold logical chunk
   // (i%8) ^ lds_swz(8J + i/8); that depends on the parity of J, hence two offsets.
@@ -156,112 +183,142 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 #pragma unroll
   for (int par = 0; par < 2; ++par)
     lane_off[par] = (uint32_t)((lane >> 3) * K + (((lane & 7) ^ lds_swz<GEMM_BK>(8 * par + (lane >> 3))) << 4));
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(w8 + (int64_t)n0 * K), 0, (int)((int64_t)(N - n0) * K), 0x00020000);
-  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a8 + (int64_t)m0 * K), 0, (int)((int64_t)(M - m0) * K), 0x00020000);
-  const int nk = (K + GEMM_BK - 1) / GEMM_BK;
+  auto rsrc = [&](const uint8_t* base, int row0, int rows) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * K), 0, (int)((int64_t)(rows - row0) * K),
+                                             0x00020000);
+  };
+  static_assert(C::THREADS >= C::BM + C::BN, "one thread per epilogue operand");
 
-  v16f acc[TN][TM];
-#pragma unroll
-  for (int a = 0; a < TN; ++a)
-#pragma unroll
-    for (int b = 0; b < TM; ++b)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
-
-  const int wrow0 = wn * (C::BN / C::WN), xrow0 = wm * (C::BM / C::WM);
+  int s = blockIdx.x;
+  int tm, tn;
+  tile_coords(s, tiles_m, tiles_n, tm, tn);
+  __amdgpu_buffer_rsrc_t wrs = rsrc(w8, tn * C::BN, N), xrs = rsrc(a8, tm * C::BM, M);
   gemm_dma<C>(wrs, xrs, smem, lane_off, K, wave, 0);
-  for (int ks = 0; ks < nk; ++ks) {
-    uint8_t* cur = smem + (ks & 1) * C::STAGE;
-    // Stage ks is this wave's only DMA in flight.  After the barrier every wave's copy of
-    // stage ks has landed and every wave has finished stage ks-1, whose buffer then takes
-    // stage ks+1 while stage ks is multiplied.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    block_barrier();
-    if (KTAIL && ks == nk - 1) {
-      zero_tail<C>(cur, (K % GEMM_BK) >> 4);
-      block_barrier();
-    }
-    if (ks + 1 < nk) gemm_dma<C>(wrs, xrs, smem + ((ks + 1) & 1) * C::STAGE, lane_off, K, wave, (ks + 1) * GEMM_BK);
-    mma_stage<C>(cur, wrow0, xrow0, lane, acc);
-  }
+  int gs = 0;  // global stage counter: stage buffer parity runs on across tiles
 
-  // ---- epilogue ------------------------------------------------------------------------
-  // acc[a][b] register i: channel n = nb + 8 (i/4) + 4 g + i%4, token m = mb + lane%32.
-  const int g = lane >> 5;
-  const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)bias) & 7) == 0) &&
-                      ((((uintptr_t)out) & 7) == 0);
-#pragma unroll
-  for (int a = 0; a < TN; ++a) {
-    const int nb = n0 + wrow0 + 32 * a;
-    float swq[4][4], bq[4][4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = nb + 8 * q + 4 * g;
-      if (vec_ok && n + 3 < N) {
-        const v4f s4 = *reinterpret_cast<const v4f*>(sw + n);
-        swq[q][0] = s4[0]; swq[q][1] = s4[1]; swq[q][2] = s4[2]; swq[q][3] = s4[3];
-        if (bias) {
-          const uint2 b4 = *reinterpret_cast<const uint2*>(bias + n);
-          bq[q][0] = __uint_as_float(b4.x << 16); bq[q][1] = __uint_as_float(b4.x & 0xffff0000u);
-          bq[q][2] = __uint_as_float(b4.y << 16); bq[q][3] = __uint_as_float(b4.y & 0xffff0000u);
-        } else {
-          bq[q][0] = bq[q][1] = bq[q][2] = bq[q][3] = 0.0f;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int nn = min(n + e, N - 1);
-          swq[q][e] = sw[nn];
-          bq[q][e] = bias ? bf16_bits_to_f32(bias[nn]) : 0.0f;
-        }
+  for (; s < ntiles; s += gridDim.x) {
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    // the tile's channel scales, bias and token scales, read now (their latency hides
+    // behind the mainloop) and handed to the epilogue through LDS after it
+    float ep_v0 = 0.0f, ep_v1 = 0.0f;
+    if ((int)threadIdx.x < C::BN) {
+      const int n = n0 + threadIdx.x;
+      if (n < N) {
+        ep_v0 = sw[n];
+        if (bias) ep_v1 = bf16_bits_to_f32(bias[n]);
       }
+    } else if ((int)threadIdx.x < C::BN + C::BM) {
+      const int m = m0 + threadIdx.x - C::BN;
+      if (m < M) ep_v0 = sa[m];
     }
+    // the next tile of this workgroup, whose first stage is copied during this epilogue
+    const int s_next = s + gridDim.x;
+    int tm_n = 0, tn_n = 0;
+    if (s_next < ntiles) tile_coords(s_next, tiles_m, tiles_n, tm_n, tn_n);
+
+    v16f acc[TN][TM];
 #pragma unroll
-    for (int b = 0; b < TM; ++b) {
-      const int m = m0 + xrow0 + 32 * b + (lane & 31);
-      const float sam = sa[min(m, M - 1)];
-      v16f lacc;
-      if constexpr (HAS_LORA) {
-        // LoRA up-projection on the bf16 MFMA: lacc^T[n][m] = sum_j B[n][j] t[m][j]
+    for (int a = 0; a < TN; ++a)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
-        const uint16_t* brow = lora_b + (int64_t)min(nb + (lane & 31), N - 1) * lora_r + 8 * g;
-        const uint16_t* trow = lora_t + (int64_t)min(m, M - 1) * lora_r + 8 * g;
-        for (int kk = 0; kk < lora_r; kk += 16) {
-          const v8bf bo = *reinterpret_cast<const v8bf*>(brow + kk);
-          const v8bf to = *reinterpret_cast<const v8bf*>(trow + kk);
-          lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bo, to, lacc, 0, 0, 0);
-        }
+      for (int b = 0; b < TM; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+
+    for (int ks = 0; ks < nk; ++ks, ++gs) {
+      uint8_t* cur = smem + (gs & 1) * C::STAGE;
+      uint8_t* nxt = smem + ((gs + 1) & 1) * C::STAGE;
+      // Stage gs is this wave's only DMA in flight (and the epilogue operands, older).
+      // After the barrier every wave's copy of it has landed and every wave has finished
+      // stage gs-1, whose buffer then takes stage gs+1 while stage gs is multiplied.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      block_barrier();
+      if (KTAIL && ks == nk - 1) {
+        zero_tail<C>(cur, (K % GEMM_BK) >> 4);
+        block_barrier();
       }
-      if (m < M) {
+      if (ks + 1 < nk) {
+        gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, (ks + 1) * GEMM_BK);
+      } else if (s_next < ntiles) {
+        wrs = rsrc(w8, tn_n * C::BN, N);
+        xrs = rsrc(a8, tm_n * C::BM, M);
+        gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, 0);
+      }
+      mma_stage<C>(cur, wrow0, xrow0, lane, acc);
+    }
+
+    // ---- epilogue ----------------------------------------------------------------------
+    // (the previous tile's epilogue reads of these LDS words finished before the barrier
+    // at the top of this tile's last stage)
+    if ((int)threadIdx.x < C::BN) {
+      ep_sw[threadIdx.x] = ep_v0;
+      ep_b[threadIdx.x] = ep_v1;
+    } else if ((int)threadIdx.x < C::BN + C::BM) {
+      ep_sa[threadIdx.x - C::BN] = ep_v0;
+    }
+    block_barrier();
+
+    // acc[a][b] register i: channel n = nb + 8 (i/4) + 4 g + i%4, token m = mb + lane%32.
+    const int g = lane >> 5;
+    const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)out) & 7) == 0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = nb + 8 * q + 4 * g;
-          uint32_t o[4];
+    for (int a = 0; a < TN; ++a) {
+      const int nl = wrow0 + 32 * a;  // tile-local channel base
+      const int nb = n0 + nl;
+      v4f swq[4], bq[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = acc[a][b][4 * q + e] * sam * swq[q][e] + bq[q][e];
-            v = bf16r(v);
-            if constexpr (HAS_LORA) {
-              const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
-              v = bf16r(v + br);
+      for (int q = 0; q < 4; ++q) {
+        swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl + 8 * q + 4 * g);
+        bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl + 8 * q + 4 * g);
+      }
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int ml = xrow0 + 32 * b + (lane & 31);
+        const int m = m0 + ml;
+        const float sam = ep_sa[ml];
+        v16f lacc;
+        if constexpr (HAS_LORA) {
+          // LoRA up-projection on the bf16 MFMA: lacc^T[n][m] = sum_j B[n][j] t[m][j]
+#pragma unroll
+          for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+          const uint16_t* brow = lora_b + (int64_t)min(nb + (lane & 31), N - 1) * lora_r + 8 * g;
+          const uint16_t* trow = lora_t + (int64_t)min(m, M - 1) * lora_r + 8 * g;
+          for (int kk = 0; kk < lora_r; kk += 16) {
+            const v8bf bo = *reinterpret_cast<const v8bf*>(brow + kk);
+            const v8bf to = *reinterpret_cast<const v8bf*>(trow + kk);
+            lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bo, to, lacc, 0, 0, 0);
+          }
+        }
+        if (m < M) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = nb + 8 * q + 4 * g;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = acc[a][b][4 * q + e] * sam * swq[q][e] + bq[q][e];
+              if constexpr (HAS_LORA || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
+              if constexpr (HAS_LORA) {
+                const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
+                v[e] = bf16r(v[e] + br);
+              }
+              if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(v[e]);
             }
-            if constexpr (ACT == MXF8_ACT_GELU_TANH) v = bf16r(gelu_tanh_f32(v));
-            o[e] = f32_to_bf16_bits(v);
-          }
-          uint16_t* dst = out + (int64_t)m * ld_out + n;
-          if (vec_ok && n + 3 < N) {
-            *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-          } else {
+            const uint32_t o01 = bf16x2(v[0], v[1]), o23 = bf16x2(v[2], v[3]);
+            uint16_t* dst = out + (int64_t)m * ld_out + n;
+            if (vec_ok && n + 3 < N) {
+              *reinterpret_cast<uint2*>(dst) = make_uint2(o01, o23);
+            } else {
+              const uint16_t o[4] = {(uint16_t)o01, (uint16_t)(o01 >> 16), (uint16_t)o23, (uint16_t)(o23 >> 16)};
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) dst[e] = (uint16_t)o[e];
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) dst[e] = o[e];
+            }
           }
         }
       }
     }
+    tm = tm_n;
+    tn = tn_n;
   }
 }
 
@@ -323,12 +380,33 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
     }
 }
 
+// Compute units of the current device (cached per device; 0 if the query fails).
+static int device_cus() {
+  constexpr int kMaxDev = 64;
+  static int cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  int n = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    __atomic_store_n(&cache[dev], n, __ATOMIC_RELAXED);
+  }
+  return n;
+}
+
 template <class C, int ACT, bool LORA, bool KTAIL>
 static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
                         const uint16_t* bias, const uint16_t* lt, const uint16_t* lb, int r, float ls, uint16_t* out,
                         int M, int N, int K, int64_t ld_out, hipStream_t st) {
   const int tiles_m = (int)cdiv(M, C::BM), tiles_n = (int)cdiv(N, C::BN);
-  gemm_fp8_rowwise_kernel<C, ACT, LORA, KTAIL><<<dim3(tiles_m * tiles_n), dim3(C::THREADS), 0, st>>>(
+  const int ntiles = tiles_m * tiles_n;
+  // Persistent grid: as many workgroups as stay resident (LDS decides: one per CU for the
+  // 256 x 256 tile, two for 128 x 128), a multiple of the 8 XCDs.
+  constexpr int per_cu = (160 * 1024) / (2 * C::STAGE + (2 * C::BN + C::BM) * 4);
+  int grid = device_cus() * per_cu;
+  grid = grid >= 8 ? grid & ~7 : ntiles;
+  if (grid <= 0 || grid > ntiles) grid = ntiles;
+  gemm_fp8_rowwise_kernel<C, ACT, LORA, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
       a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n);
 }
 

@@ -74,17 +74,16 @@ __device__ __forceinline__ uint32_t bf16x2(float lo, float hi) {
 // Map a tile sequence number s to an output tile.  Workgroups are dealt to the 8 XCDs
 // round-robin and a persistent workgroup b walks s = b, b + G, b + 2G, ... (G = grid, a
 // multiple of 8), so s % 8 names the XCD: give every XCD a contiguous range of tile ids,
-// then walk that range in groups of GROUP_M token-tiles so concurrently running tiles
+// then walk that range in groups of group_m token-tiles so concurrently running tiles
 // share operand panels in the XCD's L2.
-__device__ __forceinline__ void tile_coords(int s, int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords(int s, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
   const int nwg = tiles_m * tiles_n;
   const int q = nwg >> 3, rem = nwg & 7, x = s & 7, j = s >> 3;
   const int id = (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + j;
-  constexpr int GROUP_M = 8;
-  const int per_group = GROUP_M * tiles_n;
+  const int per_group = group_m * tiles_n;
   const int g = id / per_group;
-  const int first_m = g * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int first_m = g * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
   const int in = id - g * per_group;
   tm = first_m + in % gsize;
   tn = in / gsize;
@@ -162,7 +161,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const uint8_t* __restrict__ a8, const uint8_t* __restrict__ w8, const float* __restrict__ sa,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ lora_t,
     const uint16_t* __restrict__ lora_b, int lora_r, float lora_scale, uint16_t* __restrict__ out, int M, int N,
-    int K, int64_t ld_out, int tiles_m, int tiles_n) {
+    int K, int64_t ld_out, int tiles_m, int tiles_n, int group_m) {
   constexpr int TM = C::TM, TN = C::TN;
   constexpr int EP_BYTES = (2 * C::BN + C::BM) * 4;  // channel scales, bias (fp32), token scales
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + EP_BYTES];
@@ -191,7 +190,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 
   int s = blockIdx.x;
   int tm, tn;
-  tile_coords(s, tiles_m, tiles_n, tm, tn);
+  tile_coords(s, tiles_m, tiles_n, group_m, tm, tn);
   __amdgpu_buffer_rsrc_t wrs = rsrc(w8, tn * C::BN, N), xrs = rsrc(a8, tm * C::BM, M);
   gemm_dma<C>(wrs, xrs, smem, lane_off, K, wave, 0);
   int gs = 0;  // global stage counter: stage buffer parity runs on across tiles
@@ -214,7 +213,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     // the next tile of this workgroup, whose first stage is copied during this epilogue
     const int s_next = s + gridDim.x;
     int tm_n = 0, tn_n = 0;
-    if (s_next < ntiles) tile_coords(s_next, tiles_m, tiles_n, tm_n, tn_n);
+    if (s_next < ntiles) tile_coords(s_next, tiles_m, tiles_n, group_m, tm_n, tn_n);
 
     v16f acc[TN][TM];
 #pragma unroll
@@ -406,8 +405,11 @@ static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, c
   int grid = device_cus() * per_cu;
   grid = grid >= 8 ? grid & ~7 : ntiles;
   if (grid <= 0 || grid > ntiles) grid = ntiles;
+  // Token-tiles per L2 group (measured on MI355X at M = 20280): long-K products (each
+  // panel 3 MB at K = 12288) share best in narrow groups, wide-N ones in groups of 4.
+  const int group_m = K >= 8192 ? 2 : (tiles_n >= 48 ? 4 : 8);
   gemm_fp8_rowwise_kernel<C, ACT, LORA, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
-      a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n);
+      a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n, group_m);
 }
 
 template <class C>

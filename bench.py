@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
-"""Throughput of the MI355X FP8 hot path on one DiT block at 480p (one GPU).
+"""Throughput of the MI355X FP8 hot path on one DiT block (one GPU).
 
-A step is one pass of the FP8 hot path over one DiT block's worth of synthetic inputs:
+A step is one pass of the FP8 hot path over one DiT block's worth of synthetic inputs.
+The default workload (--workload dit480) is the 480p block:
 
 * the four FP8 linears of the block at M = 20280 tokens (13 latent frames x 30 x 52
   patches), hidden 3072: QKV 3072->9216, attention-out 3072->3072, MLP-up 3072->12288
@@ -13,14 +14,25 @@ A step is one pass of the FP8 hot path over one DiT block's worth of synthetic i
   ~N(0,1) in the [B,S,H,D] storage of a fused QKV projection (permuted views), Q/K/V
   quantizers, then the attention kernel; softmax scale 1/sqrt(128), repair off.
 
-value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
-4*B*H*Sq*Sk*D for the attention) / wall time of the step, in TFLOP/s, with every input
-resident in HBM before the timed region.  Each kernel of the step is also bracketed by
-HIP events on the stream it runs on; the attention kernel (the largest one) gives the
-roofline entry.  The CPU baseline times the reference's torch CPU fallbacks (fp32
-dequant-matmul and SDPA) on a bounded sample of the same workload.
+Two more workloads measure the other DiT shapes the same way:
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+* --workload joint: joint video + audio self-attention over 20280 + 1024 tokens (B=2, the
+  second item's last 384 keys masked: its audio is 640 tokens long) and text
+  cross-attention of those 21304 queries against 512 context keys, H=24, D=128;
+* --workload dit720: the 720p block, 75600 video + 2048 audio = 77648 tokens: the four
+  FP8 linears with a rank-64 bf16 LoRA (A, B ~N(0,0.01), scale 1) fused in every
+  epilogue, and self-attention at S=77648.
+
+value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
+4*B*H*Sq*Sk*D per attention; LoRA FLOPs are reported per kernel, not counted) / wall
+time of the step, in TFLOP/s, with every input resident in HBM before the timed region.
+Each kernel of the step is also bracketed by HIP events on the stream it runs on; the
+largest attention kernel gives the roofline entry.  The CPU baseline times the
+reference's torch CPU fallbacks (fp32 dequant-matmul and SDPA) on a bounded sample and
+scales those rates to the step's FLOP mix.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload dit480|joint|dit720]
+                    [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -52,6 +64,19 @@ HEADS, HEAD_DIM = 24, 128
 # (name, in_features, out_features, fused activation)
 LINEARS = (("qkv", HIDDEN, 3 * HIDDEN, 0), ("attn_out", HIDDEN, HIDDEN, 0),
            ("mlp_up", HIDDEN, MLP, 1), ("mlp_down", MLP, HIDDEN, 0))
+# workload -> (description, linear tokens or 0, LoRA rank, attentions); an attention is
+# (name, B, Sq, Sk, masked key tail of item 1)
+WORKLOADS = {
+    "dit480": ("DiT block FP8 hot path at 480p: 4 FP8 linears (M=20280, hidden 3072, MLP 12288, "
+               "GELU-tanh on MLP-up) + FP8 flash-attention B=1 H=24 S=20280 D=128",
+               TOKENS, 0, (("attn", 1, TOKENS, TOKENS, 0),)),
+    "joint": ("joint video+audio FP8 self-attention B=2 S=20280+1024 (item 1: last 384 keys masked) + "
+              "text FP8 cross-attention B=2 Sq=21304 Sk=512, H=24 D=128",
+              0, 0, (("self", 2, 21304, 21304, 384), ("cross", 2, 21304, 512, 0))),
+    "dit720": ("DiT block FP8 hot path at 720p: 4 FP8 linears (M=77648, hidden 3072, MLP 12288, GELU-tanh "
+               "on MLP-up) with a rank-64 LoRA in every epilogue + FP8 flash-attention B=1 H=24 S=77648 D=128",
+               77648, 64, (("attn", 1, 77648, 77648, 0),)),
+}
 
 
 def log(msg: str) -> None:
@@ -74,22 +99,36 @@ def activations(torch, g, m: int, k: int, dev):
     return x.to(torch.bfloat16)
 
 
-def build_workload(torch, dev):
+def build_workload(torch, dev, tokens: int, lora_rank: int, attns):
+    """FP8Linear modules with their activations, and the Q/K/V (+ key mask) of each attention."""
     from minimaxh3_amd.kernels.fp8_linear import FP8Linear
 
     g = torch.Generator(device=dev).manual_seed(0)
     linears = []
-    for name, k, n, act in LINEARS:
-        lin = torch.nn.Linear(k, n, bias=True, device=dev, dtype=torch.bfloat16)
-        with torch.no_grad():
-            lin.weight.copy_(torch.randn((n, k), device=dev, generator=g) * 0.02)
-            lin.bias.copy_(torch.randn((n,), device=dev, generator=g) * 0.01)
-        mod = FP8Linear.from_linear(lin)
-        mod.act = act
-        linears.append((name, mod, activations(torch, g, TOKENS, k, dev)))
-    qkv = torch.randn((1, TOKENS, 3, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16)
-    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
-    return linears, (q, k, v)
+    if tokens:
+        for name, k, n, act in LINEARS:
+            lin = torch.nn.Linear(k, n, bias=True, device=dev, dtype=torch.bfloat16)
+            with torch.no_grad():
+                lin.weight.copy_(torch.randn((n, k), device=dev, generator=g) * 0.02)
+                lin.bias.copy_(torch.randn((n,), device=dev, generator=g) * 0.01)
+            mod = FP8Linear.from_linear(lin)
+            mod.act = act
+            if lora_rank:
+                a = (torch.randn((lora_rank, k), device=dev, generator=g) * 0.01).to(torch.bfloat16)
+                b = (torch.randn((n, lora_rank), device=dev, generator=g) * 0.01).to(torch.bfloat16)
+                mod.adapters.append((a, b, 1.0))
+            linears.append((name, mod, activations(torch, g, tokens, k, dev)))
+    attn_inputs = []
+    for name, b, sq, sk, tail in attns:
+        q = torch.randn((b, sq, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+        kv = torch.randn((b, sk, 2, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16)
+        k, v = (kv[:, :, i].permute(0, 2, 1, 3) for i in range(2))
+        mask = None
+        if tail:
+            mask = torch.ones((b, sk), dtype=torch.bool, device=dev)
+            mask[1, sk - tail:] = False
+        attn_inputs.append((name, q, k, v, mask))
+    return linears, attn_inputs
 
 
 class Timers:
@@ -114,7 +153,7 @@ class Timers:
         return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
 
 
-def run_step(torch, ops, linears, qkv, timers: Timers | None):
+def run_step(torch, ops, linears, attn_inputs, timers: Timers | None):
     """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make."""
     tick = timers.start if timers else (lambda n: None)
     tock = timers.stop if timers else (lambda t: None)
@@ -123,22 +162,28 @@ def run_step(torch, ops, linears, qkv, timers: Timers | None):
         t = tick(f"quant_rows[{name}]")
         x8, sa = ops.quant_rows(x)
         tock(t)
+        lt, lb, ls = None, None, 0.0
+        if mod.adapters:
+            t = tick(f"lora_down[{name}]")
+            lt, lb, ls = mod._lora_operands(x)
+            tock(t)
         t = tick(f"gemm[{name}]")
-        outs.append(ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), None, None, 0.0))
+        outs.append(ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), lt, lb, ls))
         tock(t)
-    q, k, v = qkv
-    t = tick("attn_quant_q")
-    q8, sq = ops.attn_quant_q(q, ops.softmax_c(None, HEAD_DIM))
-    tock(t)
-    t = tick("attn_kmean+quant_k")
-    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
-    tock(t)
-    t = tick("attn_quant_v")
-    v8t, sv = ops.attn_quant_v(v)
-    tock(t)
-    t = tick("attn_fwd")
-    outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, TOKENS))
-    tock(t)
+    for name, q, k, v, mask in attn_inputs:
+        sfx = "" if name == "attn" else f"[{name}]"
+        t = tick("attn_quant_q" + sfx)
+        q8, sq = ops.attn_quant_q(q, ops.softmax_c(None, HEAD_DIM))
+        tock(t)
+        t = tick("attn_kmean+quant_k" + sfx)
+        k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+        tock(t)
+        t = tick("attn_quant_v" + sfx)
+        v8t, sv = ops.attn_quant_v(v)
+        tock(t)
+        t = tick("attn_fwd" + sfx)
+        outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, -1.0, q, k.shape[2]))
+        tock(t)
     return outs
 
 
@@ -166,8 +211,9 @@ def hbm_stream_reference(torch, dev, mib: int = 1024, reps: int = 5) -> dict:
             "ms": round(ms, 4), "GB/s": round(2 * mib * (1 << 20) / ms / 1e6, 1)}
 
 
-def cpu_baseline(target_s: float = 12.0) -> dict:
-    """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix."""
+def cpu_baseline(step_lin: float, step_att: float, target_s: float = 12.0) -> dict:
+    """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix
+    (step_lin GEMM FLOPs, step_att attention FLOPs)."""
     import torch
 
     from oracle.cpu_baseline import dequant_linear, quantize_rows_torch, sdpa_fallback
@@ -198,12 +244,11 @@ def cpu_baseline(target_s: float = 12.0) -> dict:
             if el >= budget or reps >= 50:
                 return el / reps
 
-    t_lin = timed(lambda: [dequant_linear(*a) for a in lin], target_s / 2)
+    # the linear sample is skipped for a workload without linears
+    t_lin = timed(lambda: [dequant_linear(*a) for a in lin], target_s / 2) if step_lin else float("inf")
     t_att = timed(lambda: sdpa_fallback(q, k, v), target_s / 2)
     lin_rate, att_rate = lin_flops / t_lin, at_flops / t_att
-    step_lin = sum(gemm_flops(TOKENS, n, k) for _, k, n, _ in LINEARS)
-    step_att = attn_flops(1, HEADS, TOKENS, TOKENS, HEAD_DIM)
-    step_s = step_lin / lin_rate + step_att / att_rate
+    step_s = (step_lin / lin_rate if step_lin else 0.0) + step_att / att_rate
     return {
         "value": round((step_lin + step_att) / step_s / 1e12, 4),
         "unit": "TFLOP/s",
@@ -222,6 +267,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="dit480")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,56 +286,65 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _native.load()
     _native.require_gfx950(dev)
+    desc, tokens, lora_rank, attns = WORKLOADS[args.workload]
     log("[bench] HBM streaming reference")
     stream_ref = hbm_stream_reference(torch, dev)
-    log("[bench] building workload")
-    linears, qkv = build_workload(torch, dev)
+    log(f"[bench] building workload {args.workload}")
+    linears, attn_inputs = build_workload(torch, dev, tokens, lora_rank, attns)
     torch.cuda.synchronize()
 
     with torch.inference_mode():
         for i in range(args.warmup):
-            run_step(torch, ops, linears, qkv, None)
+            run_step(torch, ops, linears, attn_inputs, None)
         torch.cuda.synchronize()
         log(f"[bench] warmup done ({args.warmup} steps)")
         timers = Timers(torch)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_step(torch, ops, linears, qkv, timers)
+            run_step(torch, ops, linears, attn_inputs, timers)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
     ms_step = elapsed * 1e3 / args.steps
     kern = timers.mean_ms()
 
-    step_flops = 0.0
+    def flop_part(f, t):
+        return {"ms": round(t, 4), "TFLOP/s": round(f / t / 1e9, 1), "frac": round(f / t / 1e9 / PEAK_FP8_TFLOPS, 4)}
+
+    def byte_part(nbytes, t):
+        return {"ms": round(t, 4), "GB/s": round(nbytes / t / 1e6, 1), "frac": round(nbytes / t / 1e6 / PEAK_HBM_GBS, 4)}
+
     parts = {}
-    for name, k, n, _ in LINEARS:
-        f = gemm_flops(TOKENS, n, k)
-        step_flops += f
-        t = kern[f"gemm[{name}]"]
-        parts[f"gemm[{name}]"] = {"ms": round(t, 4), "TFLOP/s": round(f / t / 1e9, 1),
-                                  "frac": round(f / t / 1e9 / PEAK_FP8_TFLOPS, 4)}
-        qb = TOKENS * k * 3 + TOKENS * 4        # bf16 read + e4m3 write + fp32 scales
-        t = kern[f"quant_rows[{name}]"]
-        parts[f"quant_rows[{name}]"] = {"ms": round(t, 4), "GB/s": round(qb / t / 1e6, 1),
-                                        "frac": round(qb / t / 1e6 / PEAK_HBM_GBS, 4)}
-    af = attn_flops(1, HEADS, TOKENS, TOKENS, HEAD_DIM)
-    step_flops += af
-    t_attn = kern["attn_fwd"]
-    parts["attn_fwd"] = {"ms": round(t_attn, 4), "TFLOP/s": round(af / t_attn / 1e9, 1),
-                         "frac": round(af / t_attn / 1e9 / PEAK_FP8_TFLOPS, 4)}
-    nelem = HEADS * TOKENS * HEAD_DIM
-    for name, nscale in (("attn_quant_q", HEADS * math.ceil(TOKENS / 128)),
-                         ("attn_kmean+quant_k", HEADS * math.ceil(TOKENS / 128)),
-                         ("attn_quant_v", HEADS * HEAD_DIM)):
-        qb = 3 * nelem + 4 * nscale
-        t = kern[name]
-        parts[name] = {"ms": round(t, 4), "GB/s": round(qb / t / 1e6, 1),
-                       "frac": round(qb / t / 1e6 / PEAK_HBM_GBS, 4)}
-    gemm_f = step_flops - af
-    gemm_ms = sum(kern[f"gemm[{n}]"] for n, *_ in LINEARS)
+    gemm_f = gemm_ms = 0.0
+    for name, k, n, _ in (LINEARS if tokens else ()):
+        f = gemm_flops(tokens, n, k)
+        gemm_f += f
+        gemm_ms += kern[f"gemm[{name}]"]
+        parts[f"gemm[{name}]"] = flop_part(f, kern[f"gemm[{name}]"])
+        if lora_rank:
+            parts[f"gemm[{name}]"]["lora_tflop"] = round(2.0 * tokens * lora_rank * (k + n) / 1e12, 4)
+            parts[f"lora_down[{name}]"] = flop_part(2.0 * tokens * lora_rank * k, kern[f"lora_down[{name}]"])
+        # bf16 read + e4m3 write + fp32 scales
+        parts[f"quant_rows[{name}]"] = byte_part(tokens * k * 3 + tokens * 4, kern[f"quant_rows[{name}]"])
+    attn_f = attn_ms = 0.0
+    biggest = None
+    for name, b, sq, sk, _ in attns:
+        sfx = "" if name == "attn" else f"[{name}]"
+        f = attn_flops(b, HEADS, sq, sk, HEAD_DIM)
+        t = kern["attn_fwd" + sfx]
+        attn_f += f
+        attn_ms += t
+        parts["attn_fwd" + sfx] = flop_part(f, t)
+        if biggest is None or f > biggest[1]:
+            biggest = ("attn_fwd" + sfx, f, t)
+        for qname, nelem, nscale in (("attn_quant_q", b * HEADS * sq * HEAD_DIM, b * HEADS * math.ceil(sq / 128)),
+                                     ("attn_kmean+quant_k", b * HEADS * sk * HEAD_DIM, b * HEADS * math.ceil(sk / 128)),
+                                     ("attn_quant_v", b * HEADS * sk * HEAD_DIM, b * HEADS * HEAD_DIM)):
+            parts[qname + sfx] = byte_part(3 * nelem + 4 * nscale, kern[qname + sfx])
+    step_flops = gemm_f + attn_f
     value = step_flops / (ms_step * 1e-3) / 1e12
+    _, af, t_attn = biggest
     achieved = af / (t_attn * 1e-3) / 1e12
 
     line = {
@@ -306,29 +361,30 @@ def main() -> int:
         "dtype": "e4m3 (fp32 accumulate)",
         "data": "synthetic (seeded randn, random-init weights)",
         "config": {
-            "workload": "DiT block FP8 hot path at 480p: 4 FP8 linears (M=20280, hidden 3072, MLP 12288, "
-                        "GELU-tanh on MLP-up) + FP8 flash-attention B=1 H=24 S=20280 D=128",
-            "tokens": TOKENS, "hidden": HIDDEN, "mlp": MLP, "heads": HEADS, "head_dim": HEAD_DIM,
+            "workload": desc,
+            "tokens": tokens or None, "hidden": HIDDEN, "mlp": MLP, "heads": HEADS, "head_dim": HEAD_DIM,
+            "lora_rank": lora_rank or None,
             "step_tflop": round(step_flops / 1e12, 4),
         },
         "frac_of_fp8_peak": round(value / PEAK_FP8_TFLOPS, 4),
-        "gemm_tflops": round(gemm_f / (gemm_ms * 1e-3) / 1e12, 1),
-        "attn_tflops": round(achieved, 1),
+        "gemm_tflops": round(gemm_f / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
+        "attn_tflops": round(attn_f / (attn_ms * 1e-3) / 1e12, 1),
         "roofline": {
-            "kernel": "attn_fwd_kernel<128,false,false,false,bf16>",
+            "kernel": f"{biggest[0]}: attn_fwd_kernel<128,...>",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": PEAK_FP8_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
-            "traffic": round(ATTN_TRAFFIC_BYTES),
+            # counter-measured for the 480p attention only
+            "traffic": round(ATTN_TRAFFIC_BYTES) if args.workload == "dit480" else None,
         },
         "kernels": parts,
         "hbm_stream_reference": stream_ref,
     }
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline")
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_baseline(gemm_f, attn_f)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

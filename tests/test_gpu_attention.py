@@ -179,26 +179,31 @@ def test_router_routes_to_fp8_on_gpu():
         ar.configure(enabled=True, repair_tau=-1.0, min_seq=4096)
 
 
-@pytest.mark.parametrize("S,H,mask_tail", [(20280, 24, 0), (21304, 24, 384)])
-def test_full_size_sampled_tiles(S, H, mask_tail):
-    """S = 20280 (480p video) and S = 21304 (video + audio, key-masked): full GPU run,
-    oracle on sampled Q tiles of sampled heads (tiles are independent)."""
-    _say(f"full size S={S} H={H} mask_tail={mask_tail}")
+@pytest.mark.parametrize("B,Sq,Sk,H,mask_tail", [
+    (1, 20280, 20280, 24, 0),      # 480p video self-attention
+    (2, 21304, 21304, 24, 384),    # joint video + audio self-attention, item 1 key-masked
+    (2, 21304, 512, 24, 0),        # text cross-attention
+    (1, 77648, 77648, 24, 0),      # 720p video + audio self-attention
+])
+def test_full_size_sampled_tiles(B, Sq, Sk, H, mask_tail):
+    """Full-size GPU runs of the DiT attention shapes; the oracle on sampled Q tiles of
+    sampled heads (Q tiles are independent)."""
+    _say(f"full size B={B} Sq={Sq} Sk={Sk} H={H} mask_tail={mask_tail}")
     from minimaxh3_amd.kernels.fp8_attention import fp8_attention
     from minimaxh3_amd import ops
-    B, D = (1, 128) if not mask_tail else (2, 128)
+    D = 128
     g = torch.Generator(device="cuda").manual_seed(0)
-    mk = lambda: torch.randn((B, S, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
-    q, k, v = mk(), mk(), mk()
+    mk = lambda S: torch.randn((B, S, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+    q, k, v = mk(Sq), mk(Sk), mk(Sk)
     mask = None
     if mask_tail:
-        mask = torch.ones((B, S), dtype=torch.bool, device="cuda")
-        mask[1, S - mask_tail:] = False
+        mask = torch.ones((B, Sk), dtype=torch.bool, device="cuda")
+        mask[1, Sk - mask_tail:] = False
     out = fp8_attention(q, k, v, key_mask=mask)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     heads = [0, H - 1]
-    tiles = [0, (S // 128) // 2, -(-S // 128) - 1]
+    tiles = [0, (Sq // 128) // 2, -(-Sq // 128) - 1]
     for b in range(B):
         for h in heads:
             qn, kn, vn = (t[b:b + 1, h:h + 1].float().cpu().numpy() for t in (q, k, v))
@@ -210,7 +215,7 @@ def test_full_size_sampled_tiles(S, H, mask_tail):
             km = None if mask is None else mask[b:b + 1].cpu().numpy()
             ref = bf16_round(oa.attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=km, q_tiles=tiles))
             for t in tiles:
-                r0, r1 = t * 128, min(S, t * 128 + 128)
+                r0, r1 = t * 128, min(Sq, t * 128 + 128)
                 assert_attn_close(out[b, h, r0:r1].float().cpu().numpy(), ref[0, 0, r0:r1])
 
 

@@ -251,3 +251,36 @@ def test_dit_block_linear_shapes_sampled_rows(N, K):
     ref = bf16_round(ol.scaled_mm(rc, codes(w8), rs, sw.cpu().numpy(), b.float().cpu().numpy()))
     assert_gemm_close(out[rows].float().cpu().numpy(), ref)
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("N,K,gelu", [(3072, 3072, False), (12288, 3072, True)])
+def test_720p_linear_lora_sampled_rows(fl, N, K, gelu):
+    """720p DiT block (M = 75600 video + 2048 audio tokens): FP8Linear with a rank-64 LoRA
+    (A, B ~ N(0, 0.01), scale 1) fused in the epilogue, GELU-tanh on MLP-up; the whole
+    output against the oracle on sampled rows (rows are independent)."""
+    _say(f"720p linear M=77648 N={N} K={K} gelu={gelu}")
+    M, r = 77648, 64
+    g = torch.Generator(device="cuda").manual_seed(1)
+    lin = torch.nn.Linear(K, N, bias=True, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn((N, K), device="cuda", generator=g) * 0.02)
+        lin.bias.copy_(torch.randn((N,), device="cuda", generator=g) * 0.01)
+    w, b = lin.weight.detach().float().cpu().numpy(), lin.bias.detach().float().cpu().numpy()
+    mod = fl.FP8Linear.from_linear(lin)
+    A = (torch.randn((r, K), device="cuda", generator=g) * 0.01).to(torch.bfloat16)
+    B = (torch.randn((N, r), device="cuda", generator=g) * 0.01).to(torch.bfloat16)
+    mod.adapters.append((A, B, 1.0))
+    mod.act = 1 if gelu else 0
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    out = mod(x)
+    torch.cuda.synchronize()
+    assert out.shape == (M, N) and torch.isfinite(out).all()
+    rows = np.r_[0:64, 40000:40064, M - 64:M]
+    w8, sw = ol.quantize_rows(w)
+    ad = [(A.float().cpu().numpy(), B.float().cpu().numpy(), 1.0)]
+    xs = x[rows].float().cpu().numpy()
+    ref = ol.fp8_linear_forward(xs, w8, sw, b, adapters=ad, gelu=gelu)
+    assert_gemm_close(out[rows].float().cpu().numpy(), ref)
+    # the LoRA delta is visible at this tolerance
+    no_lora = ol.fp8_linear_forward(xs, w8, sw, b, gelu=gelu)
+    assert np.abs(ref - no_lora).max() > 1e-2 * np.abs(ref).max()

@@ -370,6 +370,21 @@ __device__ __forceinline__ float attn_invalid_score(float sq, float skj) {
   return -1.0e30f / fmaxf((8.0f * sq) * skj, 1.0e-8f);
 }
 
+// Whether tile [kv0, kv0 + 128) has any invalid key (wave-uniform).  A bias applies to
+// every score; a key mask only matters when one of the tile's 128 mask bytes (LDS, at
+// sAux + 1024) is zero: lanes 0-31 test one dword each for a zero byte.
+template <bool HAS_MASK, bool HAS_BIAS>
+__device__ __forceinline__ bool attn_tile_needs_mask(const uint8_t* sAux, int kv0, int Sk, int lane) {
+  if (HAS_BIAS || kv0 + 128 > Sk) return true;
+  if constexpr (!HAS_MASK) {
+    return false;
+  } else {
+    const uint32_t w = lane < 32 ? *reinterpret_cast<const uint32_t*>(sAux + 1024 + 4 * lane) : 0x01010101u;
+    const bool has_zero_byte = ((w - 0x01010101u) & ~w & 0x80808080u) != 0u;
+    return __builtin_amdgcn_ballot_w64(has_zero_byte) != 0;
+  }
+}
+
 // Invalid keys (past Sk, masked, bias <= -1e8) get attn_invalid_score; with a bias S is
 // formed explicitly as (dot * sq) * sk + bias * log2 e.
 template <bool HAS_MASK, bool HAS_BIAS>
@@ -610,7 +625,7 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     v16f s[4];
     v8i pf[2];
     AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
-    if (HAS_MASK || HAS_BIAS || kv0 + 128 > Sk)
+    if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
     const float m_new = attn_codes<HAS_BIAS>(s, cx.sqI, skj, st.m, pf);
     if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));

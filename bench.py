@@ -323,8 +323,12 @@ def main() -> int:
         gemm_ms += kern[f"gemm[{name}]"]
         parts[f"gemm[{name}]"] = flop_part(f, kern[f"gemm[{name}]"])
         if lora_rank:
-            parts[f"gemm[{name}]"]["lora_tflop"] = round(2.0 * tokens * lora_rank * (k + n) / 1e12, 4)
-            parts[f"lora_down[{name}]"] = flop_part(2.0 * tokens * lora_rank * k, kern[f"lora_down[{name}]"])
+            # the rank-r up-projection runs in the GEMM epilogue (not in its FLOP count)
+            parts[f"gemm[{name}]"]["lora_tflop"] = round(2.0 * tokens * lora_rank * n / 1e12, 4)
+            # lora_down streams x (bf16) once and writes t (bf16)
+            t_ld = kern[f"lora_down[{name}]"]
+            parts[f"lora_down[{name}]"] = dict(flop_part(2.0 * tokens * lora_rank * k, t_ld),
+                                               **{"GB/s": round((tokens * k * 2 + tokens * lora_rank * 2) / t_ld / 1e6, 1)})
         # bf16 read + e4m3 write + fp32 scales
         parts[f"quant_rows[{name}]"] = byte_part(tokens * k * 3 + tokens * 4, kern[f"quant_rows[{name}]"])
     attn_f = attn_ms = 0.0

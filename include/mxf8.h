@@ -64,7 +64,7 @@ int mxf8_quant_rows(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx,
  *   lora_b [N, r] bf16 = B:   o = bf16(o + bf16(bf16(sum_j lora_t[m,j] lora_b[n,j]) * lora_scale))
  *   act == MXF8_ACT_GELU_TANH: o = bf16(gelu_tanh(o)) after the LoRA add.
  * Requires K % 16 == 0 (the reference converts only linears with in/out % 16 == 0,
- * fp8_linear.py:146) and r % 16 == 0 when a LoRA is given.
+ * fp8_linear.py:146), K <= 2^22, and r % 16 == 0 (r <= 4096) when a LoRA is given.
  */
 int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
                       const void* bias, int act,
@@ -75,8 +75,8 @@ int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const float* sa, con
 /*
  * LoRA down-projection t = bf16(x A^T) used by the LoRA epilogue (the first matmul of
  * apply_lora_adapters, kernels/fp8_linear.py:53).
- *   x [M, K] bf16 (row stride ldx), a [r, K] bf16 row-major, t [M, r] bf16 (written).
- * Requires r % 16 == 0 and K % 8 == 0.
+ *   x [M, K] bf16 (row stride ldx >= K), a [r, K] bf16 row-major, t [M, r] bf16 (written).
+ * Requires r % 16 == 0 (r <= 4096), K % 8 == 0 and ldx % 8 == 0.
  */
 int mxf8_lora_down(const void* x, int64_t ldx, const void* a, void* t,
                    int64_t M, int64_t K, int64_t r, hipStream_t stream);

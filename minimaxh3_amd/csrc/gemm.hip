@@ -156,7 +156,36 @@ __device__ __forceinline__ void mma_stage(const uint8_t* stage, int wrow0, int x
       acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf1[b], acc[a][b], 0, 0, 0, 0, 0, 0);
 }
 
-template <class C, int ACT, bool HAS_LORA, bool KTAIL>
+__device__ __forceinline__ v8bf lds_chunk_bf16(const uint8_t* tile, int row, int chunk) {
+  return *reinterpret_cast<const v8bf*>(tile + row * GEMM_BK + ((chunk ^ lds_swz<GEMM_BK>(row)) << 4));
+}
+
+// LoRA modes of the kernel: none, operands staged in LDS (r <= 128), or read from global
+// memory in the epilogue (r > 128).
+enum { LORA_NONE = 0, LORA_LDS = 1, LORA_GLOBAL = 2 };
+
+// LoRA branch of one 32x32 output block from a LoRA chunk staged like a K stage (B rows
+// [BN x 128 bytes], then t rows [BM x 128 bytes]; 64 rank columns in bf16):
+// lacc^T[n][m] += sum_j B[n][j] t[m][j].  K step j reads logical chunk 2j + g of both.
+template <class C>
+__device__ __forceinline__ void lora_chunk_mma(const uint8_t* chunk, int wrow, int xrow, int g, v16f& lacc) {
+#pragma unroll
+  for (int j = 0; j < GEMM_BK / 32; ++j) {
+    lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_chunk_bf16(chunk, wrow, 2 * j + g),
+                                                   lds_chunk_bf16(chunk + C::BN * GEMM_BK, xrow, 2 * j + g), lacc,
+                                                   0, 0, 0);
+    // one K step's fragments at a time: the accumulators hold most of the registers
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// LM (LoRA mode): with lora_t [M, r] = bf16(x A^T) and lora_b [N, r] = B, the epilogue adds
+// the reference's LoRA branch bf16(bf16(t B^T) * lora_scale) to the bf16 linear output.
+// In LORA_LDS mode the t and B tiles (r <= 128: one or two 64-column chunks) are copied
+// like K stages: the first chunk during the last K stage, into the buffer the next tile's
+// first stage would otherwise take; that stage then goes into the buffer the last K
+// stage frees, so it still overlaps the epilogue.
+template <class C, int ACT, int LM, bool KTAIL>
 __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const uint8_t* __restrict__ a8, const uint8_t* __restrict__ w8, const float* __restrict__ sa,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ lora_t,
@@ -175,23 +204,39 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
   const int wn = wave / C::WM, wm = wave % C::WM;
   const int wrow0 = wn * (C::BN / C::WN), xrow0 = wm * (C::BM / C::WM);
   const int nk = (K + GEMM_BK - 1) / GEMM_BK;
+  const int lrow = 2 * lora_r;  // LoRA operand row bytes
+  // LoRA chunks (64 rank columns each) and the valid 16-byte chunks of the last one
+  const int nl = LM == LORA_LDS ? (lora_r + 63) / 64 : 0;
+  const int l_tail = LM == LORA_LDS ? ((lora_r & 63) * 2) >> 4 : 0;
   // DMA: lane i of instruction J (stage rows 8J..8J+7) fills LDS bytes [16 i, 16 i + 16),
   // i.e. row 8J + i/8, physical chunk i%8, which must hold logical chunk
-  // (i%8) ^ lds_swz(8J + i/8); that depends on the parity of J, hence two offsets.
-  uint32_t lane_off[2];
+  // (i%8) ^ lds_swz(8J + i/8); that depends on the parity of J, hence two offsets (per
+  // source row stride: K bytes for the FP8 operands, 2r for the LoRA ones).
+  uint32_t lane_off[2], lane_off_l[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
-    lane_off[par] = (uint32_t)((lane >> 3) * K + (((lane & 7) ^ lds_swz<GEMM_BK>(8 * par + (lane >> 3))) << 4));
-  auto rsrc = [&](const uint8_t* base, int row0, int rows) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * K), 0, (int)((int64_t)(rows - row0) * K),
-                                             0x00020000);
+  for (int par = 0; par < 2; ++par) {
+    const uint32_t c = (uint32_t)(((lane & 7) ^ lds_swz<GEMM_BK>(8 * par + (lane >> 3))) << 4);
+    lane_off[par] = (uint32_t)((lane >> 3) * K) + c;
+    lane_off_l[par] = LM == LORA_LDS ? (uint32_t)((lane >> 3) * lrow) + c : 0u;
+  }
+  // buffer resource over one tile's rows [row0, row0 + span) of an operand with `rows`
+  // rows: rows past the end read as zero, and the byte range stays far below 2^31
+  auto rsrc_s = [&](const void* base, int row0, int rows, int span, int stride) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + (int64_t)row0 * stride), 0,
+                                             min(rows - row0, span) * stride, 0x00020000);
+  };
+  auto rsrc = [&](const uint8_t* base, int row0, int rows, int span) { return rsrc_s(base, row0, rows, span, K); };
+  // LoRA chunk c of tile (tm, tn) -> stage buffer `dst` (rank bytes [128 c, 128 c + 128))
+  auto lora_dma = [&](uint8_t* dst, int tm_, int tn_, int c) {
+    gemm_dma<C>(rsrc_s(lora_b, tn_ * C::BN, N, C::BN, lrow), rsrc_s(lora_t, tm_ * C::BM, M, C::BM, lrow), dst,
+                lane_off_l, lrow, wave, c * GEMM_BK);
   };
   static_assert(C::THREADS >= C::BM + C::BN, "one thread per epilogue operand");
 
   int s = blockIdx.x;
   int tm, tn;
   tile_coords(s, tiles_m, tiles_n, group_m, tm, tn);
-  __amdgpu_buffer_rsrc_t wrs = rsrc(w8, tn * C::BN, N), xrs = rsrc(a8, tm * C::BM, M);
+  __amdgpu_buffer_rsrc_t wrs = rsrc(w8, tn * C::BN, N, C::BN), xrs = rsrc(a8, tm * C::BM, M, C::BM);
   gemm_dma<C>(wrs, xrs, smem, lane_off, K, wave, 0);
   int gs = 0;  // global stage counter: stage buffer parity runs on across tiles
 
@@ -237,12 +282,40 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
       }
       if (ks + 1 < nk) {
         gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, (ks + 1) * GEMM_BK);
+      } else if (LM == LORA_LDS) {
+        lora_dma(nxt, tm, tn, 0);
       } else if (s_next < ntiles) {
-        wrs = rsrc(w8, tn_n * C::BN, N);
-        xrs = rsrc(a8, tm_n * C::BM, M);
+        wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
+        xrs = rsrc(a8, tm_n * C::BM, M, C::BM);
         gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, 0);
       }
       mma_stage<C>(cur, wrow0, xrow0, lane, acc);
+    }
+
+    // ---- LoRA chunks (LDS mode) ---------------------------------------------------------
+    // chunk 0 is in buffer gs & 1; the last K stage's buffer (gs + 1) & 1 is free once
+    // every wave has passed the barrier below
+    uint8_t* const lch0 = smem + (gs & 1) * C::STAGE;
+    uint8_t* const lch1 = smem + ((gs + 1) & 1) * C::STAGE;
+    if constexpr (LM == LORA_LDS) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      block_barrier();
+      if (nl == 2) {
+        // second chunk (r > 64): its copy is exposed; the next tile's first stage waits
+        // for the end of the epilogue
+        lora_dma(lch1, tm, tn, 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        block_barrier();
+      } else if (s_next < ntiles) {
+        wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
+        xrs = rsrc(a8, tm_n * C::BM, M, C::BM);
+        gemm_dma<C>(wrs, xrs, lch1, lane_off, K, wave, 0);
+      }
+      if (l_tail) {
+        // rank columns past r in the last chunk hold the next rows' values: zero them
+        zero_tail<C>(nl == 2 ? lch1 : lch0, l_tail);
+        block_barrier();
+      }
     }
 
     // ---- epilogue ----------------------------------------------------------------------
@@ -261,13 +334,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)out) & 7) == 0);
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
-      const int nl = wrow0 + 32 * a;  // tile-local channel base
-      const int nb = n0 + nl;
+      const int nl_ = wrow0 + 32 * a;  // tile-local channel base
+      const int nb = n0 + nl_;
       v4f swq[4], bq[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl + 8 * q + 4 * g);
-        bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl + 8 * q + 4 * g);
+        swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
+        bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
       }
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
@@ -275,10 +348,15 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         const int m = m0 + ml;
         const float sam = ep_sa[ml];
         v16f lacc;
-        if constexpr (HAS_LORA) {
-          // LoRA up-projection on the bf16 MFMA: lacc^T[n][m] = sum_j B[n][j] t[m][j]
+        if constexpr (LM != LORA_NONE) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+        }
+        if constexpr (LM == LORA_LDS) {
+          lora_chunk_mma<C>(lch0, nl_ + (lane & 31), ml, g, lacc);
+          if (nl == 2) lora_chunk_mma<C>(lch1, nl_ + (lane & 31), ml, g, lacc);
+        } else if constexpr (LM == LORA_GLOBAL) {
+          // LoRA up-projection on the bf16 MFMA from global memory (r > 128)
           const uint16_t* brow = lora_b + (int64_t)min(nb + (lane & 31), N - 1) * lora_r + 8 * g;
           const uint16_t* trow = lora_t + (int64_t)min(m, M - 1) * lora_r + 8 * g;
           for (int kk = 0; kk < lora_r; kk += 16) {
@@ -295,8 +373,10 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               v[e] = acc[a][b][4 * q + e] * sam * swq[q][e] + bq[q][e];
-              if constexpr (HAS_LORA || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
-              if constexpr (HAS_LORA) {
+              // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch *
+              // scale, bf16 sum; GELU-tanh acts on the bf16 result
+              if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
+              if constexpr (LM != LORA_NONE) {
                 const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
                 v[e] = bf16r(v[e] + br);
               }
@@ -316,66 +396,118 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         }
       }
     }
+    if constexpr (LM == LORA_LDS) {
+      if (nl == 2) {
+        // both buffers held LoRA chunks: once every wave is done with them, copy the next
+        // tile's first stage into buffer gs & 1, where its mainloop starts
+        if (s_next < ntiles) {
+          block_barrier();
+          wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
+          xrs = rsrc(a8, tm_n * C::BM, M, C::BM);
+          gemm_dma<C>(wrs, xrs, lch0, lane_off, K, wave, 0);
+        }
+      } else {
+        ++gs;  // the next tile's first stage went into buffer (gs + 1) & 1
+      }
+    }
     tm = tm_n;
     tn = tn_n;
   }
 }
 
 // ---- LoRA down-projection t = bf16(x A^T): x [M,K] bf16, A [r,K] bf16 -> t [M,r] -----
-// One wave per 32 rows of x and all r columns (r/32 accumulators, r <= 128).  K is
-// consumed 64 at a time; lane group g holds the contiguous elements [32 g, 32 g + 32) of
-// that slice for both operands (a consistent K permutation, so the sum is unchanged).
+// A workgroup computes 128 rows of t by up to 128 rank columns (blockIdx.y selects columns
+// [128 y, 128 y + 128)) on 4 waves of 32 rows, RT accumulators of 32 columns each.  K is
+// consumed 64 elements (128 bytes per row) per stage: the x tile (128 rows) and the A tile
+// (32 RT rows) are copied global -> LDS with the DMA into two stage buffers in the GEMM's
+// row layout, so the four waves share one copy of A.  K step j of a stage reads logical
+// chunk 2j + g of both operands (a consistent K permutation).
+constexpr int LD_BM = 128;
+
 template <int RT>
-__global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                        const uint16_t* __restrict__ a, uint16_t* __restrict__ t,
-                                                        int M, int K, int r) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int m0 = (blockIdx.x * 4 + wave) * 32;
-  if (m0 >= M) return;
-  const int g = lane >> 5;
-  const uint16_t* xr = x + (int64_t)min(m0 + (lane & 31), M - 1) * ldx + 32 * g;
-  const uint16_t* ar[RT];
+__global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restrict__ x, int ldxb,
+                                                        const uint8_t* __restrict__ a, uint16_t* __restrict__ t, int M,
+                                                        int K, int r) {
+  constexpr int AR = 32 * RT, STAGE = (LD_BM + AR) * GEMM_BK;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int m0 = blockIdx.x * LD_BM, j0 = blockIdx.y * 128;
+  const int Kb = 2 * K;
+  const int nk = (K + 63) / 64;
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + (int64_t)m0 * ldxb), 0, min(M - m0, LD_BM) * ldxb, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ars =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a + (int64_t)j0 * Kb), 0, min(r - j0, AR) * Kb, 0x00020000);
+  // lane i of a DMA instruction J fills tile row 8J + i/8, physical chunk i%8 = logical
+  // chunk (i%8) ^ lds_swz(row); the swizzle depends on the parity of J
+  uint32_t xoff[2], aoff[2];
 #pragma unroll
-  for (int u = 0; u < RT; ++u) ar[u] = a + (int64_t)min(32 * u + (lane & 31), r - 1) * K + 32 * g;
+  for (int par = 0; par < 2; ++par) {
+    const uint32_t c = (uint32_t)(((lane & 7) ^ lds_swz<GEMM_BK>(8 * par + (lane >> 3))) << 4);
+    xoff[par] = (uint32_t)((lane >> 3) * ldxb) + c;
+    aoff[par] = (uint32_t)((lane >> 3) * Kb) + c;
+  }
+  auto dma = [&](uint8_t* st, int kb0) {
+#pragma unroll
+    for (int j = 0; j < LD_BM / 32; ++j) {
+      const int J = (LD_BM / 32) * wave + j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, LDS_PTR(st + J * 1024), 16, xoff[J & 1], 8 * J * ldxb + kb0, 0,
+                                               0);
+    }
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int J = RT * wave + j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, LDS_PTR(st + LD_BM * GEMM_BK + J * 1024), 16, aoff[J & 1],
+                                               8 * J * Kb + kb0, 0, 0);
+    }
+  };
   v16f acc[RT];
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[u][i] = 0.0f;
-  const bool k64 = (K % 64) == 0;
-  for (int k0 = 0; k0 < K; k0 += 64) {
-    v8bf xo[4], ao[RT][4];
-    const bool full = k64 || (k0 + 64 <= K);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int kk = k0 + 32 * g + 8 * c;  // this lane's 8 elements
-      if (full || kk + 8 <= K) {
-        xo[c] = *reinterpret_cast<const v8bf*>(xr + k0 + 8 * c);
-#pragma unroll
-        for (int u = 0; u < RT; ++u) ao[u][c] = *reinterpret_cast<const v8bf*>(ar[u] + k0 + 8 * c);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          xo[c][e] = (__bf16)0.0f;
-#pragma unroll
-          for (int u = 0; u < RT; ++u) ao[u][c][e] = (__bf16)0.0f;
-        }
+  const int g = lane >> 5, xr = 32 * wave + (lane & 31);
+  dma(smem, 0);
+  for (int ks = 0; ks < nk; ++ks) {
+    uint8_t* cur = smem + (ks & 1) * STAGE;
+    // stage ks is this wave's only DMA in flight; after the barrier every wave's copy of
+    // it has landed and every wave has finished stage ks - 1, whose buffer takes ks + 1
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    block_barrier();
+    if (ks == nk - 1 && (K & 63)) {
+      // zero the chunks at or past K (they hold the next row's elements)
+      const int valid = (K & 63) >> 3;
+      for (int e = threadIdx.x; e < (LD_BM + AR) * 8; e += 256) {
+        const int row = e >> 3, c = e & 7, trow = row < LD_BM ? row : row - LD_BM;
+        if (c >= valid)
+          *reinterpret_cast<v4i*>(cur + row * GEMM_BK + ((c ^ lds_swz<GEMM_BK>(trow)) << 4)) = v4i{0, 0, 0, 0};
       }
+      block_barrier();
     }
+    if (ks + 1 < nk) dma(smem + ((ks + 1) & 1) * STAGE, (ks + 1) * GEMM_BK);
+    const uint8_t* tA = cur + LD_BM * GEMM_BK;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int j = 0; j < GEMM_BK / 32; ++j) {
+      const v8bf xf = lds_chunk_bf16(cur, xr, 2 * j + g);
 #pragma unroll
-      for (int u = 0; u < RT; ++u) acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao[u][c], xo[c], acc[u], 0, 0, 0);
+      for (int u = 0; u < RT; ++u)
+        acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_chunk_bf16(tA, 32 * u + (lane & 31), 2 * j + g), xf,
+                                                         acc[u], 0, 0, 0);
+    }
   }
-  // acc[u] is t^T: rows j = 32u + 8(i/4) + 4g + i%4, column m = m0 + lane%32
-  const int m = m0 + (lane & 31);
+  // acc[u] is t^T: rank column j = j0 + 32 u + 8 (i/4) + 4 g + i%4, row m = m0 + xr
+  const int m = m0 + xr;
   if (m >= M) return;
 #pragma unroll
   for (int u = 0; u < RT; ++u)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = 32 * u + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (j < r) t[(int64_t)m * r + j] = (uint16_t)f32_to_bf16_bits(acc[u][i]);
+    for (int q = 0; q < 4; ++q) {
+      const int j = j0 + 32 * u + 8 * q + 4 * g;  // r % 16 == 0: j < r covers j + 3
+      if (j < r) {
+        const v16f& c = acc[u];
+        *reinterpret_cast<uint2*>(t + (int64_t)m * r + j) =
+            make_uint2(bf16x2(c[4 * q], c[4 * q + 1]), bf16x2(c[4 * q + 2], c[4 * q + 3]));
+      }
     }
 }
 
@@ -393,7 +525,7 @@ static int device_cus() {
   return n;
 }
 
-template <class C, int ACT, bool LORA, bool KTAIL>
+template <class C, int ACT, int LM, bool KTAIL>
 static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
                         const uint16_t* bias, const uint16_t* lt, const uint16_t* lb, int r, float ls, uint16_t* out,
                         int M, int N, int K, int64_t ld_out, hipStream_t st) {
@@ -408,28 +540,28 @@ static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, c
   // Token-tiles per L2 group (measured on MI355X at M = 20280): long-K products (each
   // panel 3 MB at K = 12288) share best in narrow groups, wide-N ones in groups of 4.
   const int group_m = K >= 8192 ? 2 : (tiles_n >= 48 ? 4 : 8);
-  gemm_fp8_rowwise_kernel<C, ACT, LORA, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
+  gemm_fp8_rowwise_kernel<C, ACT, LM, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
       a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n, group_m);
 }
 
 template <class C>
-static void gemm_dispatch_tile(int act, bool lora, bool ktail, const uint8_t* a8, const uint8_t* w8,
+static void gemm_dispatch_tile(int act, int lm, bool ktail, const uint8_t* a8, const uint8_t* w8,
                                const float* sa, const float* sw, const uint16_t* bias, const uint16_t* lt,
                                const uint16_t* lb, int r, float ls, uint16_t* out, int M, int N, int K,
                                int64_t ld_out, hipStream_t st) {
 #define MXF8_GEMM_CASE(A, L, T)                                                                 \
-  if (act == A && lora == L && ktail == T) {                                                    \
+  if (act == A && lm == L && ktail == T) {                                                      \
     launch_gemm<C, A, L, T>(a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, st); \
     return;                                                                                     \
   }
-  MXF8_GEMM_CASE(MXF8_ACT_NONE, false, false)
-  MXF8_GEMM_CASE(MXF8_ACT_NONE, false, true)
-  MXF8_GEMM_CASE(MXF8_ACT_NONE, true, false)
-  MXF8_GEMM_CASE(MXF8_ACT_NONE, true, true)
-  MXF8_GEMM_CASE(MXF8_ACT_GELU_TANH, false, false)
-  MXF8_GEMM_CASE(MXF8_ACT_GELU_TANH, false, true)
-  MXF8_GEMM_CASE(MXF8_ACT_GELU_TANH, true, false)
-  MXF8_GEMM_CASE(MXF8_ACT_GELU_TANH, true, true)
+#define MXF8_GEMM_CASES(A, L) MXF8_GEMM_CASE(A, L, false) MXF8_GEMM_CASE(A, L, true)
+  MXF8_GEMM_CASES(MXF8_ACT_NONE, LORA_NONE)
+  MXF8_GEMM_CASES(MXF8_ACT_NONE, LORA_LDS)
+  MXF8_GEMM_CASES(MXF8_ACT_NONE, LORA_GLOBAL)
+  MXF8_GEMM_CASES(MXF8_ACT_GELU_TANH, LORA_NONE)
+  MXF8_GEMM_CASES(MXF8_ACT_GELU_TANH, LORA_LDS)
+  MXF8_GEMM_CASES(MXF8_ACT_GELU_TANH, LORA_GLOBAL)
+#undef MXF8_GEMM_CASES
 #undef MXF8_GEMM_CASE
 }
 
@@ -448,18 +580,21 @@ extern "C" int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const flo
   if (K % 16) return set_error(MXF8_EINVAL, "gemm_rowwise: K=%lld must be a multiple of 16", (long long)K);
   if (ld_out < N) return set_error(MXF8_EINVAL, "gemm_rowwise: ld_out < N");
   if (act != MXF8_ACT_NONE && act != MXF8_ACT_GELU_TANH) return set_error(MXF8_EINVAL, "gemm_rowwise: bad act");
-  if (M > 0x7fffffff / 2 || N > 0x7fffffff / 2 || K > 0x7fffffff / 2)
+  // buffer ranges span one tile: 256 rows of K bytes (FP8) or 2r bytes (LoRA)
+  if (M > 0x7fffffff / 2 || N > 0x7fffffff / 2 || K > (1 << 22))
     return set_error(MXF8_EINVAL, "gemm_rowwise: shape too large");
   const bool lora = lora_t != nullptr;
   if (lora) {
     if (!lora_b) return set_error(MXF8_EINVAL, "gemm_rowwise: lora_t without lora_b");
-    if (r <= 0 || r % 16 || r > 4096) return set_error(MXF8_EINVAL, "gemm_rowwise: LoRA rank must be a positive multiple of 16");
+    if (r <= 0 || r % 16 || r > 4096)
+      return set_error(MXF8_EINVAL, "gemm_rowwise: LoRA rank must be a positive multiple of 16 (<= 4096)");
     if (((uintptr_t)lora_t % 16) || ((uintptr_t)lora_b % 16))
       return set_error(MXF8_EINVAL, "gemm_rowwise: LoRA operands must be 16-byte aligned");
   }
   if (((uintptr_t)a8 % 16) || ((uintptr_t)w8 % 16))
     return set_error(MXF8_EINVAL, "gemm_rowwise: FP8 operands must be 16-byte aligned");
   const bool ktail = (K % GEMM_BK) != 0;
+  const int lm = !lora ? LORA_NONE : (r <= 128 ? LORA_LDS : LORA_GLOBAL);
   const int iM = (int)M, iN = (int)N, iK = (int)K;
   const uint16_t* b16 = static_cast<const uint16_t*>(bias);
   const uint16_t* lt = static_cast<const uint16_t*>(lora_t);
@@ -468,11 +603,11 @@ extern "C" int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const flo
   // 256x256 tiles when they fill the chip, 128x128 otherwise.
   const int64_t big_tiles = cdiv(M, 256) * cdiv(N, 256);
   if (big_tiles >= 2 * 256)
-    gemm_dispatch_tile<GemmBig>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
-                                 ld_out, stream);
+    gemm_dispatch_tile<GemmBig>(act, lm, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
+                                ld_out, stream);
   else
-    gemm_dispatch_tile<GemmSmall>(act, lora, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
-                                 ld_out, stream);
+    gemm_dispatch_tile<GemmSmall>(act, lm, ktail, a8, w8, sa, sw, b16, lt, lb, (int)r, lora_scale, o16, iM, iN, iK,
+                                  ld_out, stream);
   return check_launch("gemm_rowwise");
 }
 
@@ -481,19 +616,25 @@ extern "C" int mxf8_lora_down(const void* x, int64_t ldx, const void* a, void* t
   if (M < 0 || K <= 0 || r <= 0) return set_error(MXF8_EINVAL, "lora_down: bad shape");
   if (M == 0) return MXF8_OK;
   if (!x || !a || !t) return set_error(MXF8_EINVAL, "lora_down: null pointer");
-  if (r % 16 || r > 128) return set_error(MXF8_EINVAL, "lora_down: r must be a multiple of 16 and <= 128");
-  if (K % 8 || ldx % 8 || ((uintptr_t)x % 16) || ((uintptr_t)a % 16))
-    return set_error(MXF8_EINVAL, "lora_down: K, ldx must be multiples of 8 and operands 16-byte aligned");
-  if (M > 0x7fffffff / 2 || K > 0x7fffffff / 2) return set_error(MXF8_EINVAL, "lora_down: shape too large");
-  const dim3 grid((unsigned)cdiv(M, 128));
-  const uint16_t* x16 = static_cast<const uint16_t*>(x);
-  const uint16_t* a16 = static_cast<const uint16_t*>(a);
+  if (r % 16 || r > 4096) return set_error(MXF8_EINVAL, "lora_down: r must be a multiple of 16 and <= 4096");
+  if (K % 8 || ldx % 8 || ldx < K || ((uintptr_t)x % 16) || ((uintptr_t)a % 16) || ((uintptr_t)t % 8))
+    return set_error(MXF8_EINVAL, "lora_down: K, ldx must be multiples of 8 (ldx >= K) and operands aligned");
+  // per-workgroup buffer ranges are 128 rows of x and 128 rows of A
+  if (M > 0x7fffffff / 2 || ldx > 0x7fffffff / (2 * LD_BM) || K > 0x7fffffff / (2 * 128))
+    return set_error(MXF8_EINVAL, "lora_down: shape too large");
+  const dim3 grid((unsigned)cdiv(M, LD_BM), (unsigned)cdiv(r, 128));
+  const uint8_t* xb = static_cast<const uint8_t*>(x);
+  const uint8_t* ab = static_cast<const uint8_t*>(a);
   uint16_t* t16 = static_cast<uint16_t*>(t);
-  if (r <= 32)
-    lora_down_kernel<1><<<grid, 256, 0, stream>>>(x16, ldx, a16, t16, (int)M, (int)K, (int)r);
-  else if (r <= 64)
-    lora_down_kernel<2><<<grid, 256, 0, stream>>>(x16, ldx, a16, t16, (int)M, (int)K, (int)r);
+  const int rs = (int)(r < 128 ? r : 128);  // rank columns per workgroup
+  const int ldxb = (int)(2 * ldx);
+  if (rs <= 32)
+    lora_down_kernel<1><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
+  else if (rs <= 64)
+    lora_down_kernel<2><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
+  else if (rs <= 96)
+    lora_down_kernel<3><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
   else
-    lora_down_kernel<4><<<grid, 256, 0, stream>>>(x16, ldx, a16, t16, (int)M, (int)K, (int)r);
+    lora_down_kernel<4><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
   return check_launch("lora_down");
 }

@@ -53,12 +53,27 @@ def test_gemm_rejects_bad_ld_and_act(lib):
     assert lib.mxf8_gemm_rowwise(d, d, d, d, None, 7, None, None, 0, 0.0, d, 4, 8, 32, 8, None) == 1
     assert lib.mxf8_gemm_rowwise(d, d, d, d, None, 0, d, d, 20, 1.0, d, 4, 8, 32, 8, None) == 1
     assert "rank" in _err(lib)
+    assert lib.mxf8_gemm_rowwise(d, d, d, d, None, 0, d, d, 4112, 1.0, d, 4, 8, 32, 8, None) == 1
+    assert "rank" in _err(lib)
+    assert lib.mxf8_gemm_rowwise(d, d, d, d, None, 0, d, None, 64, 1.0, d, 4, 8, 32, 8, None) == 1
+    assert "lora_b" in _err(lib)
+    assert lib.mxf8_gemm_rowwise(d, d, d, d, None, 0, None, None, 0, 0.0, d, 4, 8, (1 << 22) + 16, 8, None) == 1
+    assert "too large" in _err(lib)
 
 
 def test_empty_shapes_are_no_ops(lib):
     assert lib.mxf8_gemm_rowwise(None, None, None, None, None, 0, None, None, 0, 0.0, None, 0, 8, 32, 8, None) == 0
     assert lib.mxf8_quant_rows(None, 0, 0, 16, 16, None, None, None) == 0
     assert lib.mxf8_lora_down(None, 16, None, None, 0, 16, 16, None) == 0
+
+
+def test_lora_down_argument_checks(lib):
+    d = ctypes.c_void_p(256)
+    assert lib.mxf8_lora_down(d, 16, d, d, 4, 16, 24, None) == 1      # r % 16
+    assert lib.mxf8_lora_down(d, 16, d, d, 4, 16, 4112, None) == 1    # r > 4096
+    assert lib.mxf8_lora_down(d, 16, d, d, 4, 12, 16, None) == 1      # K % 8
+    assert lib.mxf8_lora_down(d, 8, d, d, 4, 16, 16, None) == 1       # ldx < K
+    assert lib.mxf8_lora_down(None, 16, d, d, 4, 16, 16, None) == 1   # null x
 
 
 def test_quant_rows_argument_checks(lib):

@@ -221,11 +221,51 @@ def test_lora_down_matches_bf16_matmul():
     _say("lora_down")
     from minimaxh3_amd import ops
     rng = np.random.default_rng(10)
-    for M, K, r in ((100, 3072, 64), (33, 520, 16), (257, 1024, 128), (64, 64, 48)):
-        x, A = bf16_randn(rng, (M, K)), bf16_randn(rng, (r, K), 0.05)
-        t = ops.lora_down(to_gpu(x), to_gpu(A)).float().cpu().numpy()
-        ref = bf16_round((x.astype(np.float64) @ A.astype(np.float64).T).astype(np.float32))
+    # (M, K, r, ldx): K tails (520, 64 + 8), ranks below / above one 128-column workgroup
+    # slice (192: two slices, the second half full), strided rows
+    for M, K, r, ldx in ((100, 3072, 64, 3072), (33, 520, 16, 520), (257, 1024, 128, 1024), (64, 64, 48, 64),
+                         (300, 72, 192, 72), (130, 256, 80, 320)):
+        xf = bf16_randn(rng, (M, ldx))
+        x = xf[:, :K]
+        A = bf16_randn(rng, (r, K), 0.05)
+        xg = to_gpu(xf)[:, :K]
+        assert xg.stride(0) == ldx
+        t = ops.lora_down(xg, to_gpu(A)).float().cpu().numpy()
+        dot = x.astype(np.float64) @ A.astype(np.float64).T
+        ref = bf16_round(dot.astype(np.float32))
         np.testing.assert_allclose(t, ref, rtol=2 ** -7, atol=1e-3 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("M,N,K,r,gelu", [
+    (300, 640, 768, 64, False),      # 128 x 128 tiles, one 64-column LoRA chunk in LDS
+    (1100, 1280, 528, 128, True),    # K tail stage, two LoRA chunks, GELU on the bf16 output
+    (4096, 8192, 256, 64, False),    # 256 x 256 tiles
+    (500, 384, 256, 80, False),      # second chunk partly past r (zeroed in LDS)
+    (200, 256, 256, 16, True),       # first chunk partly past r
+    (300, 512, 256, 192, False),     # r > 128: operands read from global memory
+])
+def test_gemm_lora_epilogue_matches_oracle(M, N, K, r, gelu):
+    """The GEMM's LoRA epilogue (t = bf16(x A^T), B, scale) against the reference branch
+    bf16(bf16(bf16(t B^T) * scale) + bf16(linear)); the branch must be visible at the
+    tolerance."""
+    _say(f"gemm lora epilogue M={M} N={N} K={K} r={r} gelu={gelu}")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(M + r)
+    x = with_outliers(rng, bf16_randn(rng, (M, K)))
+    w = bf16_randn(rng, (N, K), 0.02)
+    b = bf16_randn(rng, (N,), 0.01)
+    A, B, scale = bf16_randn(rng, (r, K), 0.08), bf16_randn(rng, (N, r), 0.08), 0.75
+    xg = to_gpu(x)
+    x8, sa = ops.quant_rows(xg)
+    w8, sw = ops.quant_rows(to_gpu(w))
+    lt = ops.lora_down(xg, to_gpu(A))
+    out = ops.gemm_rowwise(x8, w8, sa, sw.view(1, -1), to_gpu(b), int(gelu), lt, to_gpu(B), scale)
+    out = out.float().cpu().numpy()
+    w8c, swc = ol.quantize_rows(w)
+    ref = ol.fp8_linear_forward(x, w8c, swc, b, adapters=[(A, B, scale)], gelu=gelu)
+    assert_gemm_close(out, ref)
+    no_lora = ol.fp8_linear_forward(x, w8c, swc, b, gelu=gelu)
+    assert np.abs(ref - no_lora).max() > 5e-2 * np.abs(ref).max()
 
 
 # ---------------------------------------------------------------- full-size shapes (properties)

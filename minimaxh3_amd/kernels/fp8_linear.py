@@ -83,6 +83,27 @@ class FP8Linear(nn.Module):
         linear.bias = None
         return mod
 
+    @classmethod
+    @torch.no_grad()
+    def from_quantized(cls, w8: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
+                       device: torch.device | str | None = None) -> "FP8Linear":
+        """FP8Linear from stored buffers: e4m3 codes ``w8 [N, K]``, per-output-channel fp32
+        scales ``w_scale`` ([N] or [1, N]) and an optional bias [N] (stored as bf16).  These
+        are the buffers ``from_linear`` computes; no quantization runs."""
+        if w8.dtype != torch.float8_e4m3fn or w8.ndim != 2:
+            raise ValueError("from_quantized: w8 must be a 2D float8_e4m3fn tensor")
+        N, K = w8.shape
+        if w_scale.dtype != torch.float32 or w_scale.numel() != N:
+            raise ValueError(f"from_quantized: w_scale must hold {N} fp32 scales")
+        if bias is not None and bias.numel() != N:
+            raise ValueError(f"from_quantized: bias must hold {N} values")
+        dev = torch.device(device) if device is not None else w8.device
+        mod = cls(K, N)
+        mod.register_buffer("w8", w8.to(dev).contiguous())
+        mod.register_buffer("w_scale", w_scale.to(dev).reshape(1, N).contiguous())
+        mod.register_buffer("bias", None if bias is None else bias.to(dev, torch.bfloat16).reshape(N).contiguous())
+        return mod
+
     def _lora_operands(self, x2d: torch.Tensor):
         """(t = bf16(x A^T), B, scale) for the fused epilogue, or (None, None, 0.0).
 

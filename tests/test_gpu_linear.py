@@ -217,6 +217,37 @@ def test_fp8linear_two_adapters_odd_rank(fl):
     assert_gemm_close(out, ref)
 
 
+def test_fp8_checkpoint_roundtrip_bit_identical(fl, tmp_path):
+    """convert_transformer_to_fp8 on the GPU (with the GELU fold), save_fp8_checkpoint, then
+    load_fp8_checkpoint into a fresh bf16 copy: bit-identical forward outputs, and every
+    loaded module's codes and scales equal the oracle's per-row quantization of the
+    original weight."""
+    _say("fp8 checkpoint roundtrip")
+    import copy
+    from minimaxh3_amd.kernels import fp8_checkpoint as ck
+    from tests.test_module_surgery import Toy
+    torch.manual_seed(0)
+    base = Toy().to("cuda", torch.bfloat16)
+    conv = copy.deepcopy(base)
+    n = fl.convert_transformer_to_fp8(conv, "to_k", keep_edge_blocks=1, fuse_gelu=True)
+    x = torch.randn(3, 40, 64, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        y1 = conv(x)
+    path = str(tmp_path / "toy_fp8.safetensors")
+    assert ck.save_fp8_checkpoint(conv, path) == n == 20
+    fresh = copy.deepcopy(base)
+    assert ck.load_fp8_checkpoint(fresh, path, fuse_gelu=True) == n
+    with torch.no_grad():
+        y2 = fresh(x)
+    assert torch.equal(y1, y2)
+    for name, m in fresh.named_modules():
+        if isinstance(m, fl.FP8Linear):
+            assert m.w8.is_cuda
+            w8, sw = ol.quantize_rows(base.get_submodule(name).weight.detach().float().cpu().numpy())
+            np.testing.assert_array_equal(codes(m.w8), w8)
+            np.testing.assert_array_equal(m.w_scale.cpu().numpy().ravel(), sw.ravel())
+
+
 def test_lora_down_matches_bf16_matmul():
     _say("lora_down")
     from minimaxh3_amd import ops

@@ -21,7 +21,9 @@ Two more workloads measure the other DiT shapes the same way:
   cross-attention of those 21304 queries against 512 context keys, H=24, D=128;
 * --workload dit720: the 720p block, 75600 video + 2048 audio = 77648 tokens: the four
   FP8 linears with a rank-64 bf16 LoRA (A, B ~N(0,0.01), scale 1) fused in every
-  epilogue, and self-attention at S=77648.
+  epilogue, and self-attention at S=77648.  The QKV and MLP-up inputs are the adaLN
+  modulation LayerNorm(x) * (1 + scale) + shift (shift, scale ~N(0,0.1)) of the block's
+  hidden state, made with their e4m3 codes by the fused adaLN quantizer.
 
 value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
 4*B*H*Sq*Sk*D per attention; LoRA FLOPs are reported per kernel, not counted) / wall
@@ -64,18 +66,21 @@ HEADS, HEAD_DIM = 24, 128
 # (name, in_features, out_features, fused activation)
 LINEARS = (("qkv", HIDDEN, 3 * HIDDEN, 0), ("attn_out", HIDDEN, HIDDEN, 0),
            ("mlp_up", HIDDEN, MLP, 1), ("mlp_down", MLP, HIDDEN, 0))
-# workload -> (description, linear tokens or 0, LoRA rank, attentions); an attention is
-# (name, B, Sq, Sk, masked key tail of item 1)
+# workload -> (description, linear tokens or 0, LoRA rank, attentions, adaLN inputs); an
+# attention is (name, B, Sq, Sk, masked key tail of item 1); with adaLN the QKV and MLP-up
+# inputs are LayerNorm(x) * (1 + scale) + shift, made by the fused adaLN quantizer
+ADALN_LINEARS = ("qkv", "mlp_up")
 WORKLOADS = {
     "dit480": ("DiT block FP8 hot path at 480p: 4 FP8 linears (M=20280, hidden 3072, MLP 12288, "
                "GELU-tanh on MLP-up) + FP8 flash-attention B=1 H=24 S=20280 D=128",
-               TOKENS, 0, (("attn", 1, TOKENS, TOKENS, 0),)),
+               TOKENS, 0, (("attn", 1, TOKENS, TOKENS, 0),), False),
     "joint": ("joint video+audio FP8 self-attention B=2 S=20280+1024 (item 1: last 384 keys masked) + "
               "text FP8 cross-attention B=2 Sq=21304 Sk=512, H=24 D=128",
-              0, 0, (("self", 2, 21304, 21304, 384), ("cross", 2, 21304, 512, 0))),
-    "dit720": ("DiT block FP8 hot path at 720p: 4 FP8 linears (M=77648, hidden 3072, MLP 12288, GELU-tanh "
-               "on MLP-up) with a rank-64 LoRA in every epilogue + FP8 flash-attention B=1 H=24 S=77648 D=128",
-               77648, 64, (("attn", 1, 77648, 77648, 0),)),
+              0, 0, (("self", 2, 21304, 21304, 384), ("cross", 2, 21304, 512, 0)), False),
+    "dit720": ("DiT block FP8 hot path at 720p: adaLN (shift/scale ~N(0,0.1)) fused with the FP8 quantization "
+               "of the QKV and MLP-up inputs, 4 FP8 linears (M=77648, hidden 3072, MLP 12288, GELU-tanh on "
+               "MLP-up) with a rank-64 LoRA in every epilogue + FP8 flash-attention B=1 H=24 S=77648 D=128",
+               77648, 64, (("attn", 1, 77648, 77648, 0),), True),
 }
 
 
@@ -99,8 +104,9 @@ def activations(torch, g, m: int, k: int, dev):
     return x.to(torch.bfloat16)
 
 
-def build_workload(torch, dev, tokens: int, lora_rank: int, attns):
-    """FP8Linear modules with their activations, and the Q/K/V (+ key mask) of each attention."""
+def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool = False):
+    """FP8Linear modules with their activations (and adaLN shift / scale [1, C] where the
+    input is adaLN-modulated), and the Q/K/V (+ key mask) of each attention."""
     from minimaxh3_amd.kernels.fp8_linear import FP8Linear
 
     g = torch.Generator(device=dev).manual_seed(0)
@@ -117,7 +123,11 @@ def build_workload(torch, dev, tokens: int, lora_rank: int, attns):
                 a = (torch.randn((lora_rank, k), device=dev, generator=g) * 0.01).to(torch.bfloat16)
                 b = (torch.randn((n, lora_rank), device=dev, generator=g) * 0.01).to(torch.bfloat16)
                 mod.adapters.append((a, b, 1.0))
-            linears.append((name, mod, activations(torch, g, tokens, k, dev)))
+            mod_params = None
+            if adaln and name in ADALN_LINEARS:
+                mod_params = tuple((torch.randn((1, k), device=dev, generator=g) * 0.1).to(torch.bfloat16)
+                                   for _ in range(2))
+            linears.append((name, mod, activations(torch, g, tokens, k, dev), mod_params))
     attn_inputs = []
     for name, b, sq, sk, tail in attns:
         q = torch.randn((b, sq, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
@@ -158,10 +168,18 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None):
     tick = timers.start if timers else (lambda n: None)
     tock = timers.stop if timers else (lambda t: None)
     outs = []
-    for name, mod, x in linears:
-        t = tick(f"quant_rows[{name}]")
-        x8, sa = ops.quant_rows(x)
-        tock(t)
+    for name, mod, x, mod_params in linears:
+        if mod_params is None:
+            t = tick(f"quant_rows[{name}]")
+            x8, sa = ops.quant_rows(x)
+            tock(t)
+        else:
+            # x is the block's hidden state; the linear's input is its adaLN modulation
+            t = tick(f"adaln_quant[{name}]")
+            x8, sa, y = ops.adaln_quant_rows(x.unsqueeze(0), mod_params[0], mod_params[1], 1e-6, False,
+                                             bool(mod.adapters))
+            tock(t)
+            x = y
         lt, lb, ls = None, None, 0.0
         if mod.adapters:
             t = tick(f"lora_down[{name}]")
@@ -286,11 +304,11 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _native.load()
     _native.require_gfx950(dev)
-    desc, tokens, lora_rank, attns = WORKLOADS[args.workload]
+    desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]
     log("[bench] HBM streaming reference")
     stream_ref = hbm_stream_reference(torch, dev)
     log(f"[bench] building workload {args.workload}")
-    linears, attn_inputs = build_workload(torch, dev, tokens, lora_rank, attns)
+    linears, attn_inputs = build_workload(torch, dev, tokens, lora_rank, attns, adaln)
     torch.cuda.synchronize()
 
     with torch.inference_mode():
@@ -330,7 +348,12 @@ def main() -> int:
             parts[f"lora_down[{name}]"] = dict(flop_part(2.0 * tokens * lora_rank * k, t_ld),
                                                **{"GB/s": round((tokens * k * 2 + tokens * lora_rank * 2) / t_ld / 1e6, 1)})
         # bf16 read + e4m3 write + fp32 scales
-        parts[f"quant_rows[{name}]"] = byte_part(tokens * k * 3 + tokens * 4, kern[f"quant_rows[{name}]"])
+        if adaln and name in ADALN_LINEARS:
+            # bf16 read + e4m3 write + fp32 scales (+ the bf16 modulated copy the LoRA reads)
+            nbytes = tokens * k * 3 + tokens * 4 + (tokens * k * 2 if lora_rank else 0)
+            parts[f"adaln_quant[{name}]"] = byte_part(nbytes, kern[f"adaln_quant[{name}]"])
+        else:
+            parts[f"quant_rows[{name}]"] = byte_part(tokens * k * 3 + tokens * 4, kern[f"quant_rows[{name}]"])
     attn_f = attn_ms = 0.0
     biggest = None
     for name, b, sq, sk, _ in attns:

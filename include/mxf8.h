@@ -51,6 +51,23 @@ int mxf8_quant_rows(const void* x, int dtype, int64_t M, int64_t K, int64_t ldx,
                     uint8_t* x8, float* scale, hipStream_t stream);
 
 /*
+ * adaLN modulation fused with the per-row quantizer.  No counterpart in the reference's
+ * files: it fuses the DiT block's pre-linear adaLN (diffusers, outside the reference) with
+ * the activation quantization of FP8Linear.forward (kernels/fp8_linear.py:94).
+ *   x      [M, C] bf16, row stride ldx; rows of batch item b are [b S, (b + 1) S)
+ *   shift, scale  [ceil(M / S), C] bf16, row stride ldm (one row per batch item)
+ *   n = (x - mean) * rstd   (fp32 row mean, biased variance, rstd = 1 / sqrt(var + eps))
+ *   eager == 0: y = bf16(n * (1 + scale[b]) + shift[b])       (fp32, one rounding)
+ *   eager != 0: y = bf16(bf16(bf16(n) * bf16(1 + scale[b])) + shift[b])   (torch eager bf16)
+ *   x8 [M, C] e4m3 and sa [M] fp32 = quant_rows(y) (written); y [M, C] bf16 (written when
+ *   not NULL, row stride C).
+ * Requires C % 8 == 0, C <= 8192, ldx and ldm multiples of 8, 16-byte aligned operands.
+ */
+int mxf8_adaln_quant_rows(const void* x, int64_t M, int64_t C, int64_t ldx, int64_t S,
+                          const void* shift, const void* scale, int64_t ldm, float eps, int eager,
+                          uint8_t* x8, float* sa, void* y, hipStream_t stream);
+
+/*
  * Row-wise scaled FP8 GEMM with fused epilogue.
  * Replaces torch._scaled_mm(x8, w8.t(), scale_a, scale_b, bias, out_dtype=bf16)
  * (kernels/fp8_linear.py:95-102), the un-padding slice (105-106), the LoRA adds of

@@ -29,6 +29,7 @@ _SIGNATURES = {
     "mxf8_abi_version": (_i32, []),
     "mxf8_last_error": (ctypes.c_char_p, []),
     "mxf8_quant_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "mxf8_adaln_quant_rows": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _f32, _i32, _vp, _vp, _vp, _vp]),
     "mxf8_gemm_rowwise": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _f32, _vp, _i64, _i64, _i64, _i64,
                                  _vp]),
     "mxf8_lora_down": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),

@@ -141,6 +141,144 @@ static int quant_rows_dispatch(const void* x, int64_t M, int64_t K, int64_t ldx,
 }
 
 // ---------------------------------------------------------------------------------------
+// adaLN modulation fused with the per-row quantizer.  The DiT block's input to the QKV and
+// MLP-up linears is y = LN(x) * (1 + scale_b) + shift_b (LayerNorm without affine, the
+// adaLN shift / scale of the row's batch item b), which FP8Linear.forward then
+// quantizes per row (kernels/fp8_linear.py:27-42).  Here one pass reads x once and writes
+// the e4m3 codes and row scales of y (and, optionally, y itself in bf16).
+//   LN: fp32 mean and biased variance of the row, rstd = 1 / sqrt(var + eps),
+//       n = (x - mean) * rstd
+//   EAGER = false: y = bf16(n * (1 + scale) + shift) in fp32, one rounding (the fused
+//                  pointwise code of a compiled block)
+//   EAGER = true:  torch's eager bf16 op sequence, a rounding after each op:
+//                  n -> bf16, (1 + scale) -> bf16, product -> bf16, sum -> bf16
+// One wave per row with the row in registers (NC 16-byte chunks per lane).
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_rne(float f) { return (float)(__bf16)f; }
+
+template <int NC, bool EAGER, bool WRITE_Y>
+__global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t C,
+                                                               int64_t ldx, int64_t S,
+                                                               const uint16_t* __restrict__ shift,
+                                                               const uint16_t* __restrict__ scale, int64_t ldm,
+                                                               float eps, uint8_t* __restrict__ x8,
+                                                               float* __restrict__ sa, uint16_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t b = row / S;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+  const uint4* shr = reinterpret_cast<const uint4*>(shift + b * ldm);
+  const uint4* scr = reinterpret_cast<const uint4*>(scale + b * ldm);
+  const int64_t nchunk = C / 8;
+  uint4 v[NC];
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
+    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum += Elem<MXF8_BF16>::lo(w[i]) + Elem<MXF8_BF16>::hi(w[i]);
+  }
+  const float mean = __fdiv_rn(wave_sum(sum), (float)C);
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    if (idx < nchunk) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float d0 = Elem<MXF8_BF16>::lo(w[i]) - mean, d1 = Elem<MXF8_BF16>::hi(w[i]) - mean;
+        ss = __builtin_fmaf(d0, d0, ss);
+        ss = __builtin_fmaf(d1, d1, ss);
+      }
+    }
+  }
+  const float var = __fdiv_rn(wave_sum(ss), (float)C);
+  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
+  // modulate; y kept as packed bf16 in v
+  float amax = 0.0f;
+  uint16_t* yrow = WRITE_Y ? y + row * C : nullptr;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    if (idx < nchunk) {
+      const uint4 sh = shr[idx], sc = scr[idx];
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+      const uint32_t hw[4] = {sh.x, sh.y, sh.z, sh.w}, cw[4] = {sc.x, sc.y, sc.z, sc.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float yy[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float xf = h ? Elem<MXF8_BF16>::hi(w[i]) : Elem<MXF8_BF16>::lo(w[i]);
+          const float shf = h ? Elem<MXF8_BF16>::hi(hw[i]) : Elem<MXF8_BF16>::lo(hw[i]);
+          const float scf = h ? Elem<MXF8_BF16>::hi(cw[i]) : Elem<MXF8_BF16>::lo(cw[i]);
+          const float n = (xf - mean) * rstd;
+          if constexpr (EAGER)
+            yy[h] = bf16_rne(bf16_rne(bf16_rne(n) * bf16_rne(1.0f + scf)) + shf);
+          else
+            yy[h] = bf16_rne(n * (1.0f + scf) + shf);
+          amax = fmaxf(amax, fabsf(yy[h]));
+        }
+        o[i] = (__float_as_uint(yy[0]) >> 16) | (__float_as_uint(yy[1]) & 0xffff0000u);
+      }
+      v[c] = make_uint4(o[0], o[1], o[2], o[3]);
+      if constexpr (WRITE_Y) reinterpret_cast<uint4*>(yrow)[idx] = v[c];
+    }
+  }
+  amax = wave_max(amax);
+  const float s = e4m3_scale(amax);
+  const float r = __fdiv_rn(1.0f, s);
+  uint8_t* orow = x8 + row * C;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t idx = (int64_t)c * 64 + lane;
+    if (idx < nchunk) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = clamp448(div_by_scale(Elem<MXF8_BF16>::lo(w[i]), s, r));
+        f[2 * i + 1] = clamp448(div_by_scale(Elem<MXF8_BF16>::hi(w[i]), s, r));
+      }
+      *reinterpret_cast<uint2*>(orow + idx * 8) = make_uint2(cvt4_e4m3(f[0], f[1], f[2], f[3]),
+                                                             cvt4_e4m3(f[4], f[5], f[6], f[7]));
+    }
+  }
+  if (lane == 0) sa[row] = s;
+}
+
+template <int NC, bool EAGER>
+static void launch_adaln(const uint16_t* x, int64_t M, int64_t C, int64_t ldx, int64_t S, const uint16_t* sh,
+                         const uint16_t* sc, int64_t ldm, float eps, uint8_t* x8, float* sa, uint16_t* y,
+                         hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(M, 4));
+  if (y)
+    adaln_quant_rows_kernel<NC, EAGER, true><<<grid, 256, 0, st>>>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y);
+  else
+    adaln_quant_rows_kernel<NC, EAGER, false><<<grid, 256, 0, st>>>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y);
+}
+
+template <bool EAGER>
+static void adaln_dispatch(int nc, const uint16_t* x, int64_t M, int64_t C, int64_t ldx, int64_t S,
+                           const uint16_t* sh, const uint16_t* sc, int64_t ldm, float eps, uint8_t* x8, float* sa,
+                           uint16_t* y, hipStream_t st) {
+  switch (nc) {
+    case 1: launch_adaln<1, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    case 2: launch_adaln<2, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    case 4: launch_adaln<4, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    case 6: launch_adaln<6, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    case 8: launch_adaln<8, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    case 12: launch_adaln<12, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+    default: launch_adaln<16, EAGER>(x, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y, st); break;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Attention quantizers (kernels/fp8_attention.py:39-170)
 // ---------------------------------------------------------------------------------------
 
@@ -419,6 +557,33 @@ extern "C" int mxf8_quant_rows(const void* x, int dtype, int64_t M, int64_t K, i
     case MXF8_F32: return quant_rows_dispatch<MXF8_F32>(x, M, K, ldx, x8, scale, stream);
     default: return set_error(MXF8_EINVAL, "quant_rows: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int mxf8_adaln_quant_rows(const void* x, int64_t M, int64_t C, int64_t ldx, int64_t S, const void* shift,
+                                     const void* scale, int64_t ldm, float eps, int eager, uint8_t* x8, float* sa,
+                                     void* y, hipStream_t stream) {
+  if (M < 0 || C <= 0 || S <= 0) return set_error(MXF8_EINVAL, "adaln_quant_rows: bad shape");
+  if (M == 0) return MXF8_OK;
+  if (!x || !shift || !scale || !x8 || !sa) return set_error(MXF8_EINVAL, "adaln_quant_rows: null pointer");
+  if (C % 8 || ldx % 8 || ldm % 8 || ldx < C || ldm < C)
+    return set_error(MXF8_EINVAL, "adaln_quant_rows: C, ldx, ldm must be multiples of 8 with ldx, ldm >= C");
+  if (((uintptr_t)x | (uintptr_t)shift | (uintptr_t)scale | (uintptr_t)x8 | (uintptr_t)y) % 16)
+    return set_error(MXF8_EINVAL, "adaln_quant_rows: operands must be 16-byte aligned");
+  const int64_t per_lane = cdiv(C / 8, 64);
+  if (per_lane > 16) return set_error(MXF8_EINVAL, "adaln_quant_rows: C=%lld exceeds 8192", (long long)C);
+  if (cdiv(M, 4) > 0x7fffffff) return set_error(MXF8_EINVAL, "adaln_quant_rows: M too large");
+  if (!(eps >= 0.0f)) return set_error(MXF8_EINVAL, "adaln_quant_rows: eps must be >= 0");
+  const int nc = per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : per_lane <= 6 ? 6 : per_lane <= 8 ? 8
+                 : per_lane <= 12 ? 12 : 16;
+  const uint16_t* x16 = static_cast<const uint16_t*>(x);
+  const uint16_t* sh = static_cast<const uint16_t*>(shift);
+  const uint16_t* sc = static_cast<const uint16_t*>(scale);
+  uint16_t* y16 = static_cast<uint16_t*>(y);
+  if (eager)
+    adaln_dispatch<true>(nc, x16, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y16, stream);
+  else
+    adaln_dispatch<false>(nc, x16, M, C, ldx, S, sh, sc, ldm, eps, x8, sa, y16, stream);
+  return check_launch("adaln_quant_rows");
 }
 
 extern "C" int64_t mxf8_attn_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {

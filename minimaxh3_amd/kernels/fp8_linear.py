@@ -32,6 +32,30 @@ def quantize_rows(x2d: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return ops.quant_rows(x2d)
 
 
+def adaln_quantize_rows(
+    x: torch.Tensor,
+    shift: torch.Tensor,
+    scale: torch.Tensor,
+    eps: float = 1e-6,
+    eager_rounding: bool = False,
+    return_modulated: bool = False,
+):
+    """adaLN modulation fused with quantize_rows (an extension; no counterpart in the reference).
+
+    For a DiT block's pre-linear input ``y = LayerNorm(x) * (1 + scale) + shift`` (LayerNorm
+    without affine, ``x`` [B, S, C] bf16, adaLN ``shift`` / ``scale`` [B, C] bf16) this
+    returns ``quantize_rows(y)`` -- (x8 [B*S, C] e4m3, x_scale [B*S, 1] fp32) -- reading x
+    once, plus y [B*S, C] bf16 when ``return_modulated`` (needed by LoRA adapters).  y is
+    rounded to bf16 once, as the fused pointwise code of a compiled block computes it, or
+    after each op like torch's eager bf16 ops with ``eager_rounding``.  Feed the result to
+    ``FP8Linear.forward_quantized``.
+    """
+    if x.ndim != 3 or not x.is_cuda:
+        raise ValueError("adaln_quantize_rows expects a [B, S, C] CUDA tensor")
+    x8, sa, y = ops.adaln_quant_rows(x, shift, scale, float(eps), bool(eager_rounding), bool(return_modulated))
+    return (x8, sa, y) if return_modulated else (x8, sa)
+
+
 def apply_lora_adapters(
     x: torch.Tensor,
     out: torch.Tensor,
@@ -115,8 +139,13 @@ class FP8Linear(nn.Module):
         adapters = self.adapters
         if not adapters:
             return None, None, 0.0
-        key = tuple((id(A), id(B), float(s)) for A, B, s in adapters)
-        if key != self._lora_cache_key:
+        # the key holds the adapter tensors themselves (an id() of a freed tensor can be
+        # reused) and their in-place version counters
+        key = [(A, B, float(s), A._version, B._version) for A, B, s in adapters]
+        old = self._lora_cache_key
+        hit = old is not None and len(old) == len(key) and all(
+            o[0] is k[0] and o[1] is k[1] and o[2:] == k[2:] for o, k in zip(old, key))
+        if not hit:
             if len(adapters) == 1:
                 A, B, scale = adapters[0]
                 a, b = self._pad_rank(A.to(torch.bfloat16), B.to(torch.bfloat16))
@@ -148,6 +177,22 @@ class FP8Linear(nn.Module):
         out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
                                lora_scale)
         return out.reshape(*orig_shape[:-1], self.out_features).to(x.dtype)
+
+    def forward_quantized(self, x8: torch.Tensor, x_scale: torch.Tensor,
+                          x_modulated: torch.Tensor | None = None) -> torch.Tensor:
+        """``forward`` on an input quantized already (``adaln_quantize_rows``): x8 [M, K] e4m3,
+        x_scale [M, 1] fp32 -> bf16 [M, N].  LoRA adapters read the bf16 input
+        ``x_modulated`` [M, K] (``return_modulated=True``), as in ``forward``."""
+        if x8.ndim != 2 or x8.shape[1] != self.in_features:
+            raise ValueError(f"forward_quantized: expected x8 [M, {self.in_features}]")
+        lora_t = lora_b = None
+        lora_scale = 0.0
+        if self.adapters:
+            if x_modulated is None:
+                raise ValueError("forward_quantized: LoRA adapters need the bf16 input (x_modulated)")
+            lora_t, lora_b, lora_scale = self._lora_operands(x_modulated.reshape(-1, self.in_features))
+        return ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
+                                lora_scale)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, act={self.act}"

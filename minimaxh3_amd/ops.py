@@ -52,6 +52,49 @@ def _(x):
     return x.new_empty((M, K), dtype=E4M3), x.new_empty((M, 1), dtype=torch.float32)
 
 
+@torch.library.custom_op("mxf8::adaln_quant_rows", mutates_args=())
+def adaln_quant_rows(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float, eager: bool,
+                     want_y: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """adaLN modulation + per-row e4m3 quantization in one pass.
+
+    x [B, S, C] bf16, shift / scale [B, C] bf16 -> (x8 [B*S, C] e4m3, sa [B*S, 1] fp32,
+    y [B*S, C] bf16 or an empty tensor) with y = LN(x) * (1 + scale) + shift rounded to bf16
+    once (``eager=False``) or after every op like torch's eager bf16 ops (``eager=True``),
+    and (x8, sa) = quant_rows(y).
+    """
+    _prep(x, "adaln_quant_rows")
+    if x.ndim != 3 or shift.shape != (x.shape[0], x.shape[2]) or scale.shape != shift.shape:
+        raise ValueError("adaln_quant_rows: expected x [B, S, C] and shift, scale [B, C]")
+    if x.dtype != torch.bfloat16 or shift.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
+        raise ValueError("adaln_quant_rows: bf16 tensors expected")
+    B, S, C = x.shape
+    x2 = x.reshape(B * S, C)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    shift = shift if shift.stride(1) == 1 else shift.contiguous()
+    scale = scale if scale.stride(1) == 1 else scale.contiguous()
+    if shift.stride(0) != scale.stride(0):
+        shift, scale = shift.contiguous(), scale.contiguous()
+    M = B * S
+    x8 = torch.empty((M, C), dtype=E4M3, device=x.device)
+    sa = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    y = torch.empty((M, C) if want_y else (0,), dtype=torch.bfloat16, device=x.device)
+    if M > 0:
+        with torch.cuda.device(x.device):
+            N.check(N.load().mxf8_adaln_quant_rows(
+                x2.data_ptr(), M, C, x2.stride(0), S, shift.data_ptr(), scale.data_ptr(), shift.stride(0),
+                float(eps), int(bool(eager)), x8.data_ptr(), sa.data_ptr(), y.data_ptr() if want_y else None,
+                N.stream_of(x)), "adaln_quant_rows")
+    return x8, sa, y
+
+
+@adaln_quant_rows.register_fake
+def _(x, shift, scale, eps, eager, want_y):
+    B, S, C = x.shape
+    return (x.new_empty((B * S, C), dtype=E4M3), x.new_empty((B * S, 1), dtype=torch.float32),
+            x.new_empty((B * S, C) if want_y else (0,), dtype=torch.bfloat16))
+
+
 @torch.library.custom_op("mxf8::gemm_rowwise", mutates_args=())
 def gemm_rowwise(a8: torch.Tensor, w8: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor,
                  bias: torch.Tensor | None, act: int, lora_t: torch.Tensor | None,

@@ -6,6 +6,11 @@ Restates kernels/fp8_linear.py of the reference:
 * ``lora_branch_add``    <- apply_lora_adapters                    (fp8_linear.py:45-55)
 * ``gelu_tanh``          <- the tanh-GELU that follows the MLP-up linear in the DiT FFN
 * ``fp8_linear_forward`` <- FP8Linear.forward                      (fp8_linear.py:87-108)
+* ``adaln_modulate``     <- the DiT block's adaLN input to its QKV / MLP-up linears:
+  LayerNorm without affine, then x * (1 + scale) + shift (diffusers' AdaLayerNorm, a
+  dependency the reference does not vendor, model_manager.py:79-103); the values feed
+  FP8Linear.forward's quantize_rows (fp8_linear.py:94).  Pinned against torch's own
+  layer_norm and bf16 ops in tests/test_oracle_linear.py.
 """
 from __future__ import annotations
 
@@ -91,3 +96,29 @@ def fp8_linear_forward(x, w8, w_scale, bias=None, adapters=(), gelu=False):
     if gelu:
         out = bf16_round(gelu_tanh(out))
     return out
+
+
+def adaln_modulate(x, shift, scale, S, eps=1e-6, eager=False):
+    """y = LayerNorm(x) * (1 + scale_b) + shift_b for x [M, C], rows of batch item b = m // S.
+
+    LayerNorm has no affine: n = (x - mean) / sqrt(var + eps), biased variance, in float64.
+    shift, scale: [B, C] bf16 values.  ``eager=False``: y rounded to bf16 once (the fused
+    pointwise code of a compiled block).  ``eager=True``: torch's eager bf16 op sequence,
+    n -> bf16, (1 + scale) -> bf16, product -> bf16, sum -> bf16 (each op computed in fp32
+    and rounded, which float64 products / sums of bf16 values cast to fp32 reproduce).
+    Returns y as fp32 holding bf16 values.
+    """
+    x = np.asarray(x, np.float64)
+    M, C = x.shape
+    b = np.arange(M) // S
+    sh = np.asarray(shift, np.float64)[b]
+    sc = np.asarray(scale, np.float64)[b]
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    n = (x - mean) / np.sqrt(var + eps)
+    if not eager:
+        return bf16_round((n * (1.0 + sc) + sh).astype(F32))
+    nb = bf16_round(n.astype(F32)).astype(np.float64)
+    op = bf16_round((1.0 + sc).astype(F32)).astype(np.float64)
+    prod = bf16_round((nb * op).astype(F32)).astype(np.float64)
+    return bf16_round((prod + sh).astype(F32))

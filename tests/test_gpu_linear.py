@@ -4,6 +4,7 @@ import sys
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import linear as ol
 from oracle.numerics import bf16_round, e4m3_decode
@@ -355,3 +356,143 @@ def test_720p_linear_lora_sampled_rows(fl, N, K, gelu):
     # the LoRA delta is visible at this tolerance
     no_lora = ol.fp8_linear_forward(xs, w8, sw, b, gelu=gelu)
     assert np.abs(ref - no_lora).max() > 1e-2 * np.abs(ref).max()
+
+
+# ---------------------------------------------------------------- adaLN modulation + quantization
+
+def _assert_ln_close(y, ref, what):
+    """LayerNorm output bar: equal almost everywhere; elsewhere within 1 bf16 ulp, or within
+    2^-17 absolute where n (1 + scale) and shift cancel (the result's ulp is then far below
+    the operands' fp32 rounding)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    mag = np.maximum(np.abs(y), np.abs(ref))
+    ulp = np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 7), 2.0 ** -133)
+    err = np.abs(y - ref)
+    bad = (err > ulp) & (err > 2.0 ** -17)
+    assert not bad.any(), (what, err[bad][:5], y[bad][:5], ref[bad][:5])
+    assert (err > 0).mean() < 5e-3, (what, (err > 0).mean())
+
+
+def _eager_modulate(nb, shift_rows, scale_rows):
+    """torch's eager bf16 ops after the LayerNorm output nb (bf16 values)."""
+    op = bf16_round((1.0 + scale_rows.astype(np.float64)).astype(np.float32)).astype(np.float64)
+    prod = bf16_round((nb.astype(np.float64) * op).astype(np.float32)).astype(np.float64)
+    return bf16_round((prod + shift_rows).astype(np.float32))
+
+
+def _assert_eager_from_ln_neighbours(y, nb, shift_rows, scale_rows, what):
+    """Eager bar: the LayerNorm output the kernel rounded to bf16 lies within 1 bf16 ulp of
+    nb, and everything after it is exact bf16 arithmetic, so y must equal the eager
+    modulation of one of nb's neighbours (and of nb itself almost everywhere)."""
+    bits = np.ascontiguousarray(nb, np.float32).view(np.uint32).astype(np.int64)
+    ok = np.zeros(y.shape, bool)
+    for d in (0, -0x10000, 0x10000):
+        c = np.clip(bits + d, 0, 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+        hit = _eager_modulate(c, shift_rows, scale_rows) == y
+        if d == 0:
+            assert hit.mean() > 1 - 5e-3, (what, hit.mean())
+        ok |= hit
+    assert ok.all(), (what, y[~ok][:5])
+
+
+@pytest.mark.parametrize("eager", [False, True])
+def test_adaln_quant_closed_form_bit_exact(fl, eager):
+    """Rows of +-a with eps = 0 have an exact LayerNorm (+-1): y, codes and scales are then
+    fixed by the modulation and the quantizer alone and must match the oracle bit for bit."""
+    _say(f"adaln closed form eager={eager}")
+    rng = np.random.default_rng(2)
+    B, S, C = 3, 40, 3072
+    sign = np.tile(np.r_[np.ones(C // 2), -np.ones(C // 2)], (B * S, 1))
+    for r in range(B * S):
+        rng.shuffle(sign[r])
+    a = 2.0 ** rng.integers(-3, 4, size=(B * S, 1))
+    x = (sign * a).astype(np.float32).reshape(B, S, C)
+    shift = bf16_randn(rng, (B, C), 0.1)
+    scale = bf16_randn(rng, (B, C), 0.1)
+    x8, sa, y = fl.adaln_quantize_rows(to_gpu(x), to_gpu(shift), to_gpu(scale), eps=0.0, eager_rounding=eager,
+                                       return_modulated=True)
+    ref_y = ol.adaln_modulate(x.reshape(-1, C), shift, scale, S, eps=0.0, eager=eager)
+    np.testing.assert_array_equal(y.float().cpu().numpy(), ref_y)
+    rc, rs = ol.quantize_rows(ref_y)
+    np.testing.assert_array_equal(codes(x8), rc)
+    np.testing.assert_array_equal(sa.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("B,S,C", [(2, 300, 3072), (1, 77, 1000), (3, 5, 8192), (2, 1, 64)])
+def test_adaln_quant_general_rows(fl, B, S, C):
+    """DiT-like rows (offset mean, outlier channels): y within 1 bf16 ulp of the oracle (fp32
+    vs float64 LayerNorm statistics), almost always equal; codes and scales bit-exact against
+    the row quantizer applied to the kernel's own y; x8 / sa independent of writing y."""
+    _say(f"adaln general B={B} S={S} C={C}")
+    rng = np.random.default_rng(B * S + C)
+    x = bf16_randn(rng, (B, S, C), 1.5) + 0.25
+    x[..., rng.choice(C, max(1, C // 100), replace=False)] *= 20.0
+    x = bf16_round(x)
+    shift = bf16_randn(rng, (B, C), 0.1)
+    scale = bf16_randn(rng, (B, C), 0.1)
+    for eager in (False, True):
+        x8, sa, y = fl.adaln_quantize_rows(to_gpu(x), to_gpu(shift), to_gpu(scale), eager_rounding=eager,
+                                           return_modulated=True)
+        yk = y.float().cpu().numpy()
+        if eager:
+            x64 = x.reshape(-1, C).astype(np.float64)
+            mean = x64.mean(axis=1, keepdims=True)
+            n = (x64 - mean) / np.sqrt(((x64 - mean) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+            rows = np.arange(B * S) // S
+            _assert_eager_from_ln_neighbours(yk, bf16_round(n.astype(np.float32)), shift[rows], scale[rows], eager)
+        else:
+            _assert_ln_close(yk, ol.adaln_modulate(x.reshape(-1, C), shift, scale, S), eager)
+        rc, rs = ol.quantize_rows(yk)
+        np.testing.assert_array_equal(codes(x8), rc)
+        np.testing.assert_array_equal(sa.cpu().numpy(), rs)
+        x8b, sab = fl.adaln_quantize_rows(to_gpu(x), to_gpu(shift), to_gpu(scale), eager_rounding=eager)
+        assert torch.equal(x8b.view(torch.uint8), x8.view(torch.uint8)) and torch.equal(sab, sa)
+
+
+def test_adaln_quant_matches_torch_gpu_ops(fl):
+    """Against torch's own GPU layer_norm and bf16 ops (eager) and its fp32 form rounded once."""
+    _say("adaln vs torch gpu ops")
+    torch.manual_seed(3)
+    B, S, C, eps = 2, 500, 3072, 1e-6
+    x = (torch.randn(B, S, C, device="cuda") * 1.5 + 0.25).to(torch.bfloat16)
+    shift = (torch.randn(B, C, device="cuda") * 0.1).to(torch.bfloat16)
+    scale = (torch.randn(B, C, device="cuda") * 0.1).to(torch.bfloat16)
+    with torch.no_grad():
+        ref_e = F.layer_norm(x, (C,), eps=eps) * (1 + scale[:, None]) + shift[:, None]
+        ref_f = (F.layer_norm(x.float(), (C,), eps=eps) * (1 + scale.float()[:, None])
+                 + shift.float()[:, None]).to(torch.bfloat16)
+    rows = np.arange(B * S) // S
+    nb_torch = F.layer_norm(x, (C,), eps=eps).float().reshape(B * S, C).cpu().numpy()
+    sh, sc = shift.float().cpu().numpy()[rows], scale.float().cpu().numpy()[rows]
+    for eager, ref in ((True, ref_e), (False, ref_f)):
+        _, _, y = fl.adaln_quantize_rows(x, shift, scale, eps=eps, eager_rounding=eager, return_modulated=True)
+        yk = y.float().cpu().numpy()
+        if eager:
+            np.testing.assert_array_equal(_eager_modulate(nb_torch, sh, sc), ref.float().reshape(B * S, C).cpu().numpy())
+            _assert_eager_from_ln_neighbours(yk, nb_torch, sh, sc, eager)
+        else:
+            _assert_ln_close(yk, ref.float().reshape(B * S, C).cpu().numpy(), eager)
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_forward_quantized_equals_forward(fl, lora):
+    """FP8Linear.forward_quantized on the fused output == FP8Linear.forward on y, bit for bit."""
+    _say(f"forward_quantized lora={lora}")
+    rng = np.random.default_rng(4)
+    B, S, C, N = 2, 150, 3072, 1024
+    lin = torch.nn.Linear(C, N, bias=True).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(bf16_randn(rng, (N, C), 0.02)))
+    mod = fl.FP8Linear.from_linear(lin)
+    if lora:
+        mod.adapters.append((to_gpu(bf16_randn(rng, (64, C), 0.01)), to_gpu(bf16_randn(rng, (N, 64), 0.01)), 1.0))
+    x = to_gpu(bf16_randn(rng, (B, S, C)))
+    shift, scale = to_gpu(bf16_randn(rng, (B, C), 0.1)), to_gpu(bf16_randn(rng, (B, C), 0.1))
+    x8, sa, y = fl.adaln_quantize_rows(x, shift, scale, return_modulated=True)
+    out_q = mod.forward_quantized(x8, sa, y)
+    out = mod(y)
+    assert torch.equal(out_q, out)
+    if lora:
+        with pytest.raises(ValueError):
+            mod.forward_quantized(x8, sa)

@@ -85,3 +85,69 @@ def test_lora_branch_matches_torch_bf16():
     ref = (ot + (branch * 0.75).to(torch.bfloat16)).float().numpy()
     # torch's CPU bf16 matmul may accumulate in a different order: allow one bf16 ulp
     np.testing.assert_allclose(got, ref, rtol=2 ** -7, atol=1e-6)
+
+
+# ------------------------------------------------------------------ adaLN modulation
+
+def _bf16_ulp_diff(a, b):
+    """|a - b| in units of the bf16 ulp of max(|a|, |b|) (bf16-valued fp32 inputs)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    mag = np.maximum(np.abs(a), np.abs(b))
+    ulp = np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 7), 2.0 ** -133)
+    return np.abs(a - b) / ulp
+
+
+def test_adaln_modulate_closed_form():
+    """Rows of +-a (a a power of two, even count, eps = 0): mean 0, var a^2, LN output exactly
+    +-1, so y = bf16(+-(1 + scale) + shift) (one rounding) or
+    bf16(bf16(+-bf16(1 + scale)) + shift) (eager)."""
+    from oracle.linear import adaln_modulate
+    rng = np.random.default_rng(0)
+    B, S, C = 2, 3, 64
+    sign = np.where(rng.random((B * S, C)) < 0.5, 1.0, -1.0)
+    sign[:, : C // 2] = 1.0
+    sign[:, C // 2:] = -1.0
+    for r in range(B * S):
+        rng.shuffle(sign[r])
+    a = np.array([0.25, 4.0, 1.0, 0.5, 8.0, 2.0])[:, None]
+    x = (sign * a).astype(np.float32)
+    shift = bf16_round(rng.standard_normal((B, C)).astype(np.float32) * 0.1)
+    scale = bf16_round(rng.standard_normal((B, C)).astype(np.float32) * 0.1)
+    b = np.arange(B * S) // S
+    fused = adaln_modulate(x, shift, scale, S, eps=0.0)
+    np.testing.assert_array_equal(fused, bf16_round((sign * (1.0 + scale[b].astype(np.float64))
+                                                     + shift[b]).astype(np.float32)))
+    eager = adaln_modulate(x, shift, scale, S, eps=0.0, eager=True)
+    op = bf16_round((1.0 + scale[b].astype(np.float64)).astype(np.float32)).astype(np.float64)
+    np.testing.assert_array_equal(eager, bf16_round((sign * op + shift[b]).astype(np.float32)))
+
+
+def test_adaln_modulate_matches_torch_ops():
+    """Against torch's own CPU layer_norm and bf16 ops: eager (bf16 tensors, one rounding per
+    op) and fused (fp32 ops, one rounding).  LayerNorm statistics in fp32 (torch) and float64
+    (oracle) may round a value to the neighbouring bf16: at most 1 ulp, rarely."""
+    from oracle.linear import adaln_modulate
+    rng = np.random.default_rng(1)
+    B, S, C, eps = 2, 37, 3072, 1e-6
+    x = bf16_round((rng.standard_normal((B, S, C)) * 1.5 + 0.3).astype(np.float32))
+    x[..., rng.choice(C, 30, replace=False)] *= 20.0
+    x = bf16_round(x)
+    shift = bf16_round((rng.standard_normal((B, C)) * 0.1).astype(np.float32))
+    scale = bf16_round((rng.standard_normal((B, C)) * 0.1).astype(np.float32))
+    xt, sht, sct = (torch.from_numpy(v).to(torch.bfloat16) for v in (x, shift, scale))
+    with torch.no_grad():
+        eager_t = F.layer_norm(xt, (C,), eps=eps) * (1 + sct[:, None]) + sht[:, None]
+        fused_t = (F.layer_norm(xt.float(), (C,), eps=eps) * (1 + sct.float()[:, None]) + sht.float()[:, None])
+        fused_t = fused_t.to(torch.bfloat16)
+    for eager, ref in ((True, eager_t), (False, fused_t)):
+        y = adaln_modulate(x.reshape(B * S, C), shift, scale, S, eps=eps, eager=eager)
+        r = ref.float().numpy().reshape(B * S, C)
+        d = _bf16_ulp_diff(y, r)
+        err = np.abs(y.astype(np.float64) - r)
+        # within 1 ulp, or 2^-17 absolute where n (1 + scale) and shift cancel
+        assert ((d <= 1.0) | (err <= 2.0 ** -17)).all() and (d > 0).mean() < 5e-3, (eager, d.max())
+    # the two modes differ (the eager roundings matter)
+    ye = adaln_modulate(x.reshape(B * S, C), shift, scale, S, eps=eps, eager=True)
+    yf = adaln_modulate(x.reshape(B * S, C), shift, scale, S, eps=eps, eager=False)
+    assert (ye != yf).mean() > 0.01

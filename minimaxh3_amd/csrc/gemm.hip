@@ -21,7 +21,8 @@
 // first stage of the next tile is copied while the current tile's epilogue runs, and the
 // epilogue's channel scales, bias and token scales come from LDS (read into registers at
 // the start of the tile), so neither the pipeline fill nor a workgroup launch separates
-// two tiles.
+// two tiles.  A whole output tile (no LoRA) is staged through the freed stage buffer and
+// written as 16-byte stores of whole row segments.
 #include "common.h"
 
 namespace mxf8 {
@@ -332,8 +333,54 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     // acc[a][b] register i: channel n = nb + 8 (i/4) + 4 g + i%4, token m = mb + lane%32.
     const int g = lane >> 5;
     const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)out) & 7) == 0);
+    bool staged = false;
+    if constexpr (LM == LORA_NONE) {
+      staged = ((ld_out & 7) == 0) && ((((uintptr_t)out) & 15) == 0) && (m0 + C::BM <= M) && (n0 + C::BN <= N);
+    }
+    if (staged) {
+      // Whole tile in range: each 32-token round of this wave goes through a private 8 KB
+      // LDS region in the buffer of the last K stage (free after the barrier above; the
+      // next tile's first copy into it waits for the barrier at the top of its first
+      // stage), then leaves as 16-byte stores covering whole 32 TN-channel row segments.
+      constexpr int RB = TN * 64;     // staged row bytes (32 TN bf16 channels)
+      constexpr int NCH = RB / 16;    // 16-byte chunks per staged row (chunk c at c ^ row % NCH)
+      constexpr int RPI = 64 / NCH;   // rows per 64-lane read
+      static_assert(32 * RB <= C::STAGE / C::NW, "per-wave staging region");
+      uint8_t* const wreg = smem + ((gs + 1) & 1) * C::STAGE + wave * (C::STAGE / C::NW);
+      const int r = lane & 31;
 #pragma unroll
-    for (int a = 0; a < TN; ++a) {
+      for (int b = 0; b < TM; ++b) {
+        const float sam = ep_sa[xrow0 + 32 * b + r];
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+          const int nl_ = wrow0 + 32 * a;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const v4f swq = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
+            const v4f bq = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = acc[a][b][4 * q + e] * sam * swq[e] + bq[e];
+              if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(bf16r(v[e]));
+            }
+            const int chunk = 4 * a + q;
+            *reinterpret_cast<uint2*>(wreg + r * RB + ((chunk ^ (r & (NCH - 1))) << 4) + 8 * g) =
+                make_uint2(bf16x2(v[0], v[1]), bf16x2(v[2], v[3]));
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 32 / RPI; ++i) {
+          const int row = i * RPI + lane / NCH, ch = lane % NCH;
+          const uint4 val = *reinterpret_cast<const uint4*>(wreg + row * RB + ((ch ^ (row & (NCH - 1))) << 4));
+          *reinterpret_cast<uint4*>(out + (int64_t)(m0 + xrow0 + 32 * b + row) * ld_out + n0 + wrow0 + ch * 8) = val;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < TN && !staged; ++a) {
       const int nl_ = wrow0 + 32 * a;  // tile-local channel base
       const int nb = n0 + nl_;
       v4f swq[4], bq[4];

@@ -16,7 +16,8 @@ namespace mxf8 {
 
 // Fast path: one wave per row, the whole row held in registers as NC 16-byte chunks per
 // lane (chunk c of lane l covers elements [(c*64 + l) * E, +E)).  Requires K % E == 0
-// and 16-byte aligned rows.
+// and 16-byte aligned rows.  All of the row's loads are issued before the first use (a
+// loop that folds each chunk into the max as it arrives measured 3-19% slower).
 template <int DT, int NC>
 __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const void* __restrict__ x, int64_t M, int64_t K,
                                                              int64_t ldx, uint8_t* __restrict__ x8,
@@ -29,15 +30,14 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const void* __restr
   const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const T*>(x) + row * ldx);
   const int64_t nchunk = K / E;
   uint4 v[NC];
-  float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int64_t idx = (int64_t)c * 64 + lane;
-    if (idx < nchunk) {
-      v[c] = xr[idx];
-    } else {
-      v[c] = make_uint4(0, 0, 0, 0);
-    }
+    v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
     const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -172,11 +172,14 @@ __global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* _
   const uint4* scr = reinterpret_cast<const uint4*>(scale + b * ldm);
   const int64_t nchunk = C / 8;
   uint4 v[NC];
-  float sum = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int64_t idx = (int64_t)c * 64 + lane;
     v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
     const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum += Elem<MXF8_BF16>::lo(w[i]) + Elem<MXF8_BF16>::hi(w[i]);
@@ -288,6 +291,23 @@ struct Strides4 {
 
 // Loads 8 consecutive-in-d elements of row `s` as fp32.  VEC: d contiguous and the
 // 8-element group 16-byte aligned; otherwise element-wise strided loads.
+// Raw form of load8 for the vector case: the 16 bytes of 8 consecutive-in-d elements of
+// row s (issued early, converted with cvt8 later, so several loads are in flight at once).
+template <int DT>
+__device__ __forceinline__ uint4 raw8(const void* base, const Strides4& st, int64_t s, int d0) {
+  typedef typename Elem<DT>::T T;
+  return *reinterpret_cast<const uint4*>(static_cast<const T*>(base) + s * st.s + d0);
+}
+template <int DT>
+__device__ __forceinline__ void cvt8(const uint4& v, float f[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = Elem<DT>::lo(w[i]);
+    f[2 * i + 1] = Elem<DT>::hi(w[i]);
+  }
+}
+
 template <int DT, bool VEC>
 __device__ __forceinline__ void load8(const void* base, const Strides4& st, int64_t s, int d0, float f[8]) {
   typedef typename Elem<DT>::T T;
@@ -331,11 +351,23 @@ __global__ __launch_bounds__(256) void attn_quant_qk_kernel(const void* __restri
   }
   float f[NP][8];
   float amax = 0.0f;
+  uint4 raw[VEC ? NP : 1];
+  if constexpr (VEC) {
+    // every pass's load in flight before the first use
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int64_t s = blk * 128 + rl + RPP * p;
+      raw[p] = s < S ? raw8<DT>(base, st, s, cc * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int64_t s = blk * 128 + rl + RPP * p;
     if (s < S) {
-      load8<DT, VEC>(base, st, s, cc * 8, f[p]);
+      if constexpr (VEC)
+        cvt8<DT>(raw[p], f[p]);
+      else
+        load8<DT, VEC>(base, st, s, cc * 8, f[p]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         f[p][i] = IS_K ? (f[p][i] - mu[i]) : (f[p][i] * c);
@@ -383,7 +415,24 @@ __global__ __launch_bounds__(256) void attn_colreduce_kernel(const void* __restr
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int64_t s = r0 + rl; s < r1; s += RPP) {
+  int64_t s = r0 + rl;
+  if constexpr (VEC) {
+    // 8 rows' loads in flight together; rows are folded in the same order as one at a time
+    constexpr int U = 8;
+    for (; s + (U - 1) * RPP < r1; s += U * RPP) {
+      uint4 raw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) raw[u] = raw8<DT>(base, st, s + u * RPP, cc * 8);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[8];
+        cvt8<DT>(raw[u], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = ABSMAX ? fmaxf(acc[i], fabsf(f[i])) : acc[i] + f[i];
+      }
+    }
+  }
+  for (; s < r1; s += RPP) {
     float f[8];
     load8<DT, VEC>(base, st, s, cc * 8, f);
 #pragma unroll
@@ -478,12 +527,23 @@ __global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restric
   for (int p = 0; p < NP; ++p) {
     const int kq = threadIdx.x / CPR + KQP * p;
     uint32_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // col[i]: 4 key bytes of channel cc*8+i
+    uint4 raw[VEC ? 4 : 1];
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t s = blk * 128 + kq * 4 + j;
+        raw[j] = s < S ? raw8<DT>(base, st, s, cc * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t s = blk * 128 + kq * 4 + j;
       float f[8];
       if (s < S) {
-        load8<DT, VEC>(base, st, s, cc * 8, f);
+        if constexpr (VEC)
+          cvt8<DT>(raw[j], f);
+        else
+          load8<DT, VEC>(base, st, s, cc * 8, f);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) f[i] = 0.0f;

@@ -71,10 +71,13 @@ def adaln_quant_rows(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, 
     x2 = x.reshape(B * S, C)
     if x2.stride(1) != 1:
         x2 = x2.contiguous()
-    shift = shift if shift.stride(1) == 1 else shift.contiguous()
-    scale = scale if scale.stride(1) == 1 else scale.contiguous()
-    if shift.stride(0) != scale.stride(0):
-        shift, scale = shift.contiguous(), scale.contiguous()
+    # one row stride for both (expanded / strided operands are copied)
+    if shift.stride(1) != 1 or shift.stride(0) < C or shift.stride(0) % 8:
+        shift = shift.contiguous()
+    if scale.stride(1) != 1 or scale.stride(0) != shift.stride(0):
+        scale = scale.contiguous()
+        if scale.stride(0) != shift.stride(0):
+            shift = shift.contiguous()
     M = B * S
     x8 = torch.empty((M, C), dtype=E4M3, device=x.device)
     sa = torch.empty((M, 1), dtype=torch.float32, device=x.device)

@@ -448,6 +448,12 @@ def test_adaln_quant_general_rows(fl, B, S, C):
         np.testing.assert_array_equal(sa.cpu().numpy(), rs)
         x8b, sab = fl.adaln_quantize_rows(to_gpu(x), to_gpu(shift), to_gpu(scale), eager_rounding=eager)
         assert torch.equal(x8b.view(torch.uint8), x8.view(torch.uint8)) and torch.equal(sab, sa)
+    if B > 1:
+        # one shift / scale row broadcast to every batch item (stride 0) is accepted
+        sh1, sc1 = to_gpu(shift[:1]).expand(B, C), to_gpu(scale[:1]).expand(B, C)
+        x8c, sac = fl.adaln_quantize_rows(to_gpu(x), sh1, sc1)
+        x8d, sad = fl.adaln_quantize_rows(to_gpu(x), sh1.contiguous(), sc1.contiguous())
+        assert torch.equal(x8c.view(torch.uint8), x8d.view(torch.uint8)) and torch.equal(sac, sad)
 
 
 def test_adaln_quant_matches_torch_gpu_ops(fl):

@@ -137,6 +137,33 @@ def test_gemm_rowwise_gelu():
     assert_gemm_close(out.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("ld_extra,offset", [(0, 0), (8, 0), (4, 0), (8, 4), (0, 8)])
+def test_gemm_output_stride_and_alignment(ld_extra, offset):
+    """The C ABI writes into a strided, possibly offset output: whole tiles take the store
+    staged through LDS when rows are 16-byte aligned (ld_out % 8 == 0 and a 16-byte aligned
+    base) and the direct 8-byte stores otherwise; both must give the oracle's result and
+    leave the padding columns untouched."""
+    _say(f"gemm ld_out=N+{ld_extra} offset={offset}")
+    from minimaxh3_amd import _native as N
+    rng = np.random.default_rng(11 + ld_extra + offset)
+    M, Nn, K = 1024, 2048, 512  # 256 x 256 tiles do not fill the chip: 128 x 128 tiles, all whole
+    x, x8, sa, w8, sw, b = _gemm_case(rng, M, Nn, K, True)
+    a8g = to_gpu(x8, torch.uint8)
+    w8g = to_gpu(w8, torch.uint8)
+    sag, swg, bg = to_gpu(sa, torch.float32), to_gpu(sw, torch.float32), to_gpu(b)
+    ld = Nn + ld_extra
+    buf = torch.full((offset + M * ld,), -7.0, dtype=torch.bfloat16, device="cuda")
+    lib = N.load()
+    N.check(lib.mxf8_gemm_rowwise(a8g.data_ptr(), w8g.data_ptr(), sag.data_ptr(), swg.data_ptr(), bg.data_ptr(), 0,
+                                  None, None, 0, 0.0, buf.data_ptr() + 2 * offset, M, Nn, K, ld,
+                                  torch.cuda.current_stream().cuda_stream), "gemm_rowwise")
+    torch.cuda.synchronize()
+    out = buf[offset:].view(M, ld)
+    ref = bf16_round(ol.scaled_mm(x8, w8, sa, sw, b))
+    assert_gemm_close(out[:, :Nn].float().cpu().numpy(), ref)
+    assert (buf[:offset] == -7.0).all() and (out[:, Nn:] == -7.0).all()
+
+
 def test_gemm_rejects_bad_shapes():
     from minimaxh3_amd import ops
     from minimaxh3_amd._native import NativeError

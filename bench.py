@@ -57,9 +57,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over this script's dispatches and
 # scaled by what the counters read for the 1 GiB streaming kernel of
 # hbm_stream_reference() (FETCH_SIZE reports 0.500 of the bytes read, WRITE_SIZE 1.000 of
-# the bytes written): 328108.7 KiB x 2 fetched + 122337.9 KiB written.  The algorithmic
-# traffic is 186.9 MB of Q8/K8/V8T read + 124.6 MB of output written.
-ATTN_TRAFFIC_BYTES = 328108.7 * 1024 * 2 + 122337.9 * 1024
+# the bytes written): 363128.7 KiB x 2 fetched + 124406.0 KiB written.  The algorithmic
+# traffic is 249.2 MB of bf16 Q (quantized inside the launch) and K8/V8T read + 124.6 MB
+# of output written.
+ATTN_TRAFFIC_BYTES = 363128.7 * 1024 * 2 + 124406.0 * 1024
 TOKENS = 20280                # 13 x 30 x 52
 HIDDEN, MLP = 3072, 12288
 HEADS, HEAD_DIM = 24, 128
@@ -163,7 +164,7 @@ class Timers:
         return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
 
 
-def run_step(torch, ops, linears, attn_inputs, timers: Timers | None):
+def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True):
     """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make."""
     tick = timers.start if timers else (lambda n: None)
     tock = timers.stop if timers else (lambda t: None)
@@ -190,18 +191,25 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None):
         tock(t)
     for name, q, k, v, mask in attn_inputs:
         sfx = "" if name == "attn" else f"[{name}]"
-        t = tick("attn_quant_q" + sfx)
-        q8, sq = ops.attn_quant_q(q, ops.softmax_c(None, HEAD_DIM))
-        tock(t)
+        c = ops.softmax_c(None, HEAD_DIM)
         t = tick("attn_kmean+quant_k" + sfx)
         k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
         tock(t)
         t = tick("attn_quant_v" + sfx)
         v8t, sv = ops.attn_quant_v(v)
         tock(t)
-        t = tick("attn_fwd" + sfx)
-        outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, -1.0, q, k.shape[2]))
-        tock(t)
+        if fuse_q:
+            # the Q quantizer runs inside the attention launch
+            t = tick("attn_fwd" + sfx)
+            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, -1.0, k.shape[2]))
+            tock(t)
+        else:
+            t = tick("attn_quant_q" + sfx)
+            q8, sq = ops.attn_quant_q(q, c)
+            tock(t)
+            t = tick("attn_fwd" + sfx)
+            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, -1.0, q, k.shape[2]))
+            tock(t)
     return outs
 
 
@@ -287,6 +295,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="dit480")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--separate-q-quant", action="store_true",
+                    help="quantize Q in its own launch instead of inside the attention launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "
@@ -305,6 +315,7 @@ def main() -> int:
     _native.load()
     _native.require_gfx950(dev)
     desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]
+    fuse_q = not args.separate_q_quant
     log("[bench] HBM streaming reference")
     stream_ref = hbm_stream_reference(torch, dev)
     log(f"[bench] building workload {args.workload}")
@@ -313,14 +324,14 @@ def main() -> int:
 
     with torch.inference_mode():
         for i in range(args.warmup):
-            run_step(torch, ops, linears, attn_inputs, None)
+            run_step(torch, ops, linears, attn_inputs, None, fuse_q)
         torch.cuda.synchronize()
         log(f"[bench] warmup done ({args.warmup} steps)")
         timers = Timers(torch)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, timers)
+            run_step(torch, ops, linears, attn_inputs, timers, fuse_q)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
@@ -368,7 +379,8 @@ def main() -> int:
         for qname, nelem, nscale in (("attn_quant_q", b * HEADS * sq * HEAD_DIM, b * HEADS * math.ceil(sq / 128)),
                                      ("attn_kmean+quant_k", b * HEADS * sk * HEAD_DIM, b * HEADS * math.ceil(sk / 128)),
                                      ("attn_quant_v", b * HEADS * sk * HEAD_DIM, b * HEADS * HEAD_DIM)):
-            parts[qname + sfx] = byte_part(3 * nelem + 4 * nscale, kern[qname + sfx])
+            if qname + sfx in kern:  # attn_quant_q only when Q is quantized in its own launch
+                parts[qname + sfx] = byte_part(3 * nelem + 4 * nscale, kern[qname + sfx])
     step_flops = gemm_f + attn_f
     value = step_flops / (ms_step * 1e-3) / 1e12
     _, af, t_attn = biggest

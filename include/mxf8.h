@@ -163,6 +163,24 @@ int mxf8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t,
                   int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                   hipStream_t stream);
 
+/*
+ * Q quantizer fused into the attention forward: _quantize_q_kernel + _fp8_attn_kernel
+ * (kernels/fp8_attention.py:39-77 and 185-297, launches 321-336 and 380-402) in one launch.
+ * Each workgroup quantizes its own (b, h, 128-row) Q block with the arithmetic of
+ * mxf8_attn_quant_q, so the result equals mxf8_attn_quant_q followed by mxf8_attn_fwd bit
+ * for bit, without the q8 round trip through memory.
+ *   q [B, H, Sq, D] 16-bit, of out_dtype, element strides q_strides[4]: q_strides[3] == 1,
+ *   the other three multiples of 8, q 16-byte aligned (other layouts: the two-call path).
+ *   c = softmax scale * log2(e); sq_out [B, H, ceil(Sq/128)] fp32 receives the Q scales
+ *   (NULL: not written).  Other arguments as mxf8_attn_fwd.
+ */
+int mxf8_attn_fwd_q(const void* q, const int64_t q_strides[4], float c,
+                    const uint8_t* k8, const uint8_t* v8t, const float* sk, const float* sv,
+                    const uint8_t* key_mask, const float* key_bias, float repair_tau,
+                    float* sq_out, void* out, int out_dtype, const int64_t out_strides[4],
+                    int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,8 @@ _SIGNATURES = {
     "mxf8_attn_quant_v": (_i32, [_vp, _i32, _I64x4, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "mxf8_attn_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i32, _I64x4, _i64, _i64, _i64, _i64,
                              _i64, _vp]),
+    "mxf8_attn_fwd_q": (_i32, [_vp, _I64x4, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _i32, _I64x4, _i64,
+                               _i64, _i64, _i64, _i64, _vp]),
 }
 EXPORTS = tuple(_SIGNATURES)
 

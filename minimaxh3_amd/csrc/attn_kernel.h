@@ -69,8 +69,17 @@ __device__ __forceinline__ int xcd_linear_id(int L, int total) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + kk;
 }
 
-// Per-workgroup constants of a (b, h, Q tile) work item.
-template <int D, bool HAS_MASK, bool HAS_BIAS>
+// 16-bit query for the fused Q quantizer: element (b, h, s, d) at q + b sb + h sh + s ss + d.
+struct AttnQ16 {
+  const uint16_t* q;
+  int64_t sb, sh, ss;
+  float c;        // softmax scale * log2(e)
+  float* sq_out;  // [B, H, ceil(Sq / 128)] or null
+};
+
+// Per-workgroup constants of a (b, h, Q tile) work item.  QF: the Q fragments are
+// quantized by the workgroup from 16-bit Q (quant_q) instead of read from q8 / sq.
+template <int D, bool HAS_MASK, bool HAS_BIAS, bool QF = false>
 struct AttnCtx {
   int b, h, bh, I, nk, Skp, wave, lane, qrow;
   float sqI;
@@ -99,15 +108,17 @@ struct AttnCtx {
 
     // Q fragments (B operand of S^T): query row qrow, bytes [64 hh + 32 g, +32)
     qrow = I * 128 + wave * 32 + (lane & 31);
-    const uint8_t* qp = q8 + ((int64_t)bh * Sqp + qrow) * D + 32 * g;
+    if constexpr (!QF) {
+      const uint8_t* qp = q8 + ((int64_t)bh * Sqp + qrow) * D + 32 * g;
 #pragma unroll
-    for (int hh = 0; hh < D / 64; ++hh) {
-      const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
-      const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
-      qf[hh][0] = lo[0]; qf[hh][1] = lo[1]; qf[hh][2] = lo[2]; qf[hh][3] = lo[3];
-      qf[hh][4] = hi[0]; qf[hh][5] = hi[1]; qf[hh][6] = hi[2]; qf[hh][7] = hi[3];
+      for (int hh = 0; hh < D / 64; ++hh) {
+        const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
+        const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
+        qf[hh][0] = lo[0]; qf[hh][1] = lo[1]; qf[hh][2] = lo[2]; qf[hh][3] = lo[3];
+        qf[hh][4] = hi[0]; qf[hh][5] = hi[1]; qf[hh][6] = hi[2]; qf[hh][7] = hi[3];
+      }
+      sqI = sq[(int64_t)bh * nq + I];
     }
-    sqI = sq[(int64_t)bh * nq + I];
     skh = sk + (int64_t)bh * nk;
 
     krs = __builtin_amdgcn_make_buffer_rsrc((void*)(k8 + (int64_t)bh * Skp * D), 0, Skp * D, 0x00020000);
@@ -138,6 +149,55 @@ struct AttnCtx {
                                  (((lane & 3) ^ lds_swz<64>(rr)) << 4));
       }
     }
+  }
+
+  // The Q quantizer of this work item's 128-row block, fused: q~ = fp32(q) * c, sq =
+  // max(max|q~|, 1e-12) / 448 over the block, codes e4m3(clamp(q~ / sq)) -- the arithmetic
+  // of attn_quant_qk_kernel, so fragments and scale are bit-identical to its q8 / sq.
+  // Rows >= Sq quantize as zeros.  red: 4 floats of LDS no DMA writes before the next
+  // attn_barrier.  Ends with a workgroup barrier.
+  template <int QDT>
+  __device__ __forceinline__ void quant_q(const AttnQ16& qa, int Sq, int nq, float* red) {
+    const int g = lane >> 5;
+    const bool valid = qrow < Sq;
+    const uint16_t* qp = qa.q + (int64_t)b * qa.sb + (int64_t)h * qa.sh + (int64_t)qrow * qa.ss + 32 * g;
+    uint4 raw[D / 64][4];
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        raw[hh][u] = valid ? *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u) : make_uint4(0, 0, 0, 0);
+    float f[D / 64][32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[4] = {raw[hh][u].x, raw[hh][u].y, raw[hh][u].z, raw[hh][u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[hh][8 * u + 2 * i] = Elem<QDT>::lo(w[i]) * qa.c;
+          f[hh][8 * u + 2 * i + 1] = Elem<QDT>::hi(w[i]) * qa.c;
+          amax = fmaxf(amax, fabsf(f[hh][8 * u + 2 * i]));
+          amax = fmaxf(amax, fabsf(f[hh][8 * u + 2 * i + 1]));
+        }
+      }
+    amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    attn_barrier();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = e4m3_scale(amax);
+    const float r = __fdiv_rn(1.0f, sc);
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh)
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        qf[hh][k] = (int)cvt4_e4m3(clamp448(div_by_scale(f[hh][4 * k], sc, r)),
+                                   clamp448(div_by_scale(f[hh][4 * k + 1], sc, r)),
+                                   clamp448(div_by_scale(f[hh][4 * k + 2], sc, r)),
+                                   clamp448(div_by_scale(f[hh][4 * k + 3], sc, r)));
+    sqI = sc;
+    if (qa.sq_out != nullptr && wave == 0 && lane == 0) qa.sq_out[(int64_t)bh * nq + I] = sc;
   }
 
   // Key tile (keys [kv0, kv0 + 128)) -> sK, rows permuted by key_of_row.
@@ -584,18 +644,20 @@ struct AttnOccupancy {
   static constexpr int waves = DO_REPAIR ? 1 : 2;
 };
 
-template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT>
+// QF: Q arrives as 16-bit values of the output's dtype (qa) and each workgroup quantizes
+// its own 128-row block while its first KV tile is in flight; q8 / sq are then unused.
+template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT, bool QF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOccupancy<DO_REPAIR>::waves)))
 void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
                      const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
                      const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
                      void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H, int Sq,
-                     int Sk, int nq) {
+                     int Sk, int nq, AttnQ16 qa) {
   typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * T::BUF];
-  const AttnCtx<D, HAS_MASK, HAS_BIAS> cx(q8, k8, v8t, sq, sk, key_mask, key_bias, H, Sk, nq,
-                                          xcd_linear_id(blockIdx.x, gridDim.x),
-                                          __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
+  AttnCtx<D, HAS_MASK, HAS_BIAS, QF> cx(q8, k8, v8t, sq, sk, key_mask, key_bias, H, Sk, nq,
+                                        xcd_linear_id(blockIdx.x, gridDim.x),
+                                        __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
   const int nk = cx.nk, lane = cx.lane;
   const AttnFragOfs<D> fo(lane);
 
@@ -606,6 +668,9 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
   cx.dma_k(smem, j0 * 128);
   cx.dma_v(smem + T::KB, j0 * 128);
   cx.dma_aux(smem + T::KB + T::VB, j0 * 128, Sk);
+  // The block maximum goes through the second buffer, which the first DMA into it (after
+  // the loop's first barrier) cannot reach before every wave has read it.
+  if constexpr (QF) cx.template quant_q<ODT>(qa, Sq, nq, reinterpret_cast<float*>(smem + T::BUF));
   int j = j0;
   for (int i = 0; i < nk; ++i) {
     // Tile i is the only DMA in flight; after the barrier every wave has finished tile
@@ -641,21 +706,30 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
 template <int D, bool M_, bool B_, bool R_, int ODT>
 static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t, const float* sq, const float* sk,
                         const float* sv, const uint8_t* km, const float* kb, float tau, void* out,
-                        const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, hipStream_t st) {
+                        const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa,
+                        hipStream_t st) {
   const int64_t nq = cdiv(Sq, 128);
-  attn_fwd_kernel<D, M_, B_, R_, ODT><<<dim3((unsigned)(nq * B * H)), 256, 0, st>>>(
-      q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq);
+  const dim3 grid((unsigned)(nq * B * H));
+  if (qa != nullptr)
+    attn_fwd_kernel<D, M_, B_, R_, ODT, true><<<grid, 256, 0, st>>>(
+        nullptr, k8, v8t, nullptr, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk,
+        (int)nq, *qa);
+  else
+    attn_fwd_kernel<D, M_, B_, R_, ODT, false><<<grid, 256, 0, st>>>(
+        q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
+        AttnQ16{nullptr, 0, 0, 0, 0.0f, nullptr});
 }
 
+// qa == nullptr: Q from q8 / sq; otherwise the fused Q quantizer reads qa.
 template <int D, int ODT>
 static void attn_dispatch_flags(bool hm, bool hb, bool rep, const uint8_t* q8, const uint8_t* k8,
                                 const uint8_t* v8t, const float* sq, const float* sk, const float* sv,
                                 const uint8_t* km, const float* kb, float tau, void* out, const int64_t os[4],
-                                int64_t B, int64_t H, int64_t Sq, int64_t Sk, hipStream_t st) {
-#define MXF8_ATTN_CASE(M_, B_, R_)                                                                       \
-  if (hm == M_ && hb == B_ && rep == R_) {                                                               \
-    launch_attn<D, M_, B_, R_, ODT>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os, B, H, Sq, Sk, st); \
-    return;                                                                                              \
+                                int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa, hipStream_t st) {
+#define MXF8_ATTN_CASE(M_, B_, R_)                                                                           \
+  if (hm == M_ && hb == B_ && rep == R_) {                                                                   \
+    launch_attn<D, M_, B_, R_, ODT>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os, B, H, Sq, Sk, qa, st); \
+    return;                                                                                                  \
   }
   MXF8_ATTN_CASE(false, false, false)
   MXF8_ATTN_CASE(true, false, false)
@@ -675,7 +749,7 @@ static void attn_dispatch_flags(bool hm, bool hb, bool rep, const uint8_t* q8, c
                                  const uint8_t* v8t, const float* sq, const float* sk, const float* sv,     \
                                  const uint8_t* km, const float* kb, float tau, void* out,                  \
                                  const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk,         \
-                                 hipStream_t st)
+                                 const AttnQ16* qa, hipStream_t st)
 MXF8_ATTN_DECL(128, 0);
 MXF8_ATTN_DECL(128, 1);
 MXF8_ATTN_DECL(64, 0);

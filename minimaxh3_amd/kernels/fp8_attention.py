@@ -55,6 +55,11 @@ def is_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
     return _is_gfx950(q.device)
 
 
+# Quantize Q inside the attention launch when q's layout allows it (ops.attn_fwd_q);
+# False keeps the separate Q quantizer launch.  Both give the same output bit for bit.
+fuse_q_quant = True
+
+
 def fp8_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -75,8 +80,11 @@ def fp8_attention(
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     c = ops.softmax_c(scale, D)
-    q8, sq = ops.attn_quant_q(q, c)
     mean = ops.attn_kmean(k)
     k8, sk = ops.attn_quant_k(k, mean)
     v8t, sv = ops.attn_quant_v(v)
+    if fuse_q_quant and ops.attn_fwd_q_supported(q):
+        # the attention kernel quantizes Q itself (same codes and scales as attn_quant_q)
+        return ops.attn_fwd_q(q, c, k8, v8t, sk, sv, key_mask, key_bias, float(repair_tau), Sk)
+    q8, sq = ops.attn_quant_q(q, c)
     return ops.attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, float(repair_tau), q, Sk)

@@ -266,6 +266,46 @@ def _(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, like, Sk):
     return torch.empty_like(like)
 
 
+def attn_fwd_q_supported(q: torch.Tensor) -> bool:
+    """Whether attn_fwd_q takes q's layout: 16-bit, unit channel stride, the other strides
+    multiples of 8 elements (other layouts use attn_quant_q + attn_fwd).  Reads only dtype,
+    shape and strides, which a traced graph knows for every tensor, so it causes no graph
+    break; attn_fwd_q checks the pointer's alignment when it runs."""
+    return (q.dtype in (torch.bfloat16, torch.float16) and q.dim() == 4 and q.stride(3) == 1
+            and all(s % 8 == 0 for s in q.stride()[:3]))
+
+
+@torch.library.custom_op("mxf8::attn_fwd_q", mutates_args=())
+def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, sk: torch.Tensor, sv: torch.Tensor,
+               key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, repair_tau: float,
+               Sk: int) -> torch.Tensor:
+    """attn_quant_q + attn_fwd in one launch (fp8_attention.py:321-336 and 380-402): each
+    workgroup quantizes its own 128-row Q block; same output bit for bit."""
+    _prep(q, "attn_fwd_q")
+    if not attn_fwd_q_supported(q):
+        raise ValueError("attn_fwd_q: q must be bf16/fp16 with unit channel stride, other strides multiples of 8 "
+                         "and 16-byte alignment")
+    if q.data_ptr() % 16:
+        # a view that starts off a 16-byte boundary: the two launches give the same bits
+        q8, sq = attn_quant_q(q, c)
+        return attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, q, Sk)
+    B, H, Sq, D = q.shape
+    out = torch.empty_like(q)
+    km = None if key_mask is None else key_mask.to(torch.uint8).contiguous()
+    kb = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    with torch.cuda.device(q.device):
+        N.check(N.load().mxf8_attn_fwd_q(
+            q.data_ptr(), N.strides4(q), float(c), k8.data_ptr(), v8t.data_ptr(), sk.data_ptr(), sv.data_ptr(),
+            N.ptr(km), N.ptr(kb), float(repair_tau), None, out.data_ptr(), N.dtype_code(out.dtype), N.strides4(out),
+            B, H, Sq, Sk, D, N.stream_of(q)), "attn_fwd_q")
+    return out
+
+
+@attn_fwd_q.register_fake
+def _(q, c, k8, v8t, sk, sv, key_mask, key_bias, repair_tau, Sk):
+    return torch.empty_like(q)
+
+
 def softmax_c(scale: float | None, D: int) -> float:
     """c = (scale or 1/sqrt(D)) * log2(e) (kernels/fp8_attention.py:315)."""
     return (scale if scale is not None else 1.0 / math.sqrt(D)) * 1.4426950408889634

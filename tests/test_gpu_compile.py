@@ -81,7 +81,9 @@ def test_compiled_block_one_graph_same_result(fused_adaln):
             ex = dynamo.explain(blk)(x, shift, scale)
             assert ex.graph_break_count == 0 and ex.graph_count == 1, [str(r.reason) for r in ex.break_reasons]
             targets = {str(n.target) for g in ex.graphs for n in g.graph.nodes}
-            for op in ("mxf8.gemm_rowwise", "mxf8.attn_fwd", "mxf8.attn_quant_q"):
+            # q is a view of the fused projection output, so the Q quantizer runs inside
+            # the attention launch (mxf8.attn_fwd_q)
+            for op in ("mxf8.gemm_rowwise", "mxf8.attn_fwd_q", "mxf8.attn_quant_k", "mxf8.attn_quant_v"):
                 assert any(op in t for t in targets), (op, sorted(targets))
             if fused_adaln:
                 assert any("mxf8.adaln_quant_rows" in t for t in targets)

@@ -28,13 +28,14 @@ Two more workloads measure the other DiT shapes the same way:
 value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
 4*B*H*Sq*Sk*D per attention; LoRA FLOPs are reported per kernel, not counted) / wall
 time of the step, in TFLOP/s, with every input resident in HBM before the timed region.
-Each kernel of the step is also bracketed by HIP events on the stream it runs on; the
-largest attention kernel gives the roofline entry.  The CPU baseline times the
+In the timed steps only the attention launches are bracketed by HIP events on the stream
+they run on (the largest gives the roofline entry); the per-kernel breakdown comes from
+the same number of steps run again after the timed ones with every launch bracketed.  The CPU baseline times the
 reference's torch CPU fallbacks (fp32 dequant-matmul and SDPA) on a bounded sample and
 scales those rates to the step's FLOP mix.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload dit480|joint|dit720]
-                    [--no-cpu-baseline]
+                    [--no-cpu-baseline] [--separate-q-quant]
 """
 from __future__ import annotations
 
@@ -143,18 +144,24 @@ def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool =
 
 
 class Timers:
-    """Per-kernel HIP event pairs recorded on the launching (current) stream."""
+    """Per-kernel HIP event pairs recorded on the launching (current) stream; with `prefix`,
+    only the launches whose part name starts with it are bracketed."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, prefix: str = ""):
         self.torch = torch
+        self.prefix = prefix
         self.pairs: dict[str, list] = {}
 
     def start(self, name):
+        if not name.startswith(self.prefix):
+            return None
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
         return name, e
 
     def stop(self, tok):
+        if tok is None:
+            return
         name, s = tok
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
@@ -327,16 +334,24 @@ def main() -> int:
             run_step(torch, ops, linears, attn_inputs, None, fuse_q)
         torch.cuda.synchronize()
         log(f"[bench] warmup done ({args.warmup} steps)")
-        timers = Timers(torch)
+        # The timed steps bracket only the attention launches (the roofline kernel) with HIP
+        # events: an event pair around every launch adds ~0.1 ms to a 5 ms step.
+        roof_timers = Timers(torch, prefix="attn_fwd")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, timers, fuse_q)
+            run_step(torch, ops, linears, attn_inputs, roof_timers, fuse_q)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-    log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
+        log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
+        # per-launch breakdown: the same steps again, every launch bracketed (not timed)
+        timers = Timers(torch)
+        for _ in range(args.steps):
+            run_step(torch, ops, linears, attn_inputs, timers, fuse_q)
+        torch.cuda.synchronize()
     ms_step = elapsed * 1e3 / args.steps
     kern = timers.mean_ms()
+    roof_kern = roof_timers.mean_ms()
 
     def flop_part(f, t):
         return {"ms": round(t, 4), "TFLOP/s": round(f / t / 1e9, 1), "frac": round(f / t / 1e9 / PEAK_FP8_TFLOPS, 4)}
@@ -370,7 +385,7 @@ def main() -> int:
     for name, b, sq, sk, _ in attns:
         sfx = "" if name == "attn" else f"[{name}]"
         f = attn_flops(b, HEADS, sq, sk, HEAD_DIM)
-        t = kern["attn_fwd" + sfx]
+        t = roof_kern["attn_fwd" + sfx]  # from the timed steps
         attn_f += f
         attn_ms += t
         parts["attn_fwd" + sfx] = flop_part(f, t)

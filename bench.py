@@ -396,6 +396,11 @@ def main() -> int:
                                      ("attn_quant_v", b * HEADS * sk * HEAD_DIM, b * HEADS * HEAD_DIM)):
             if qname + sfx in kern:  # attn_quant_q only when Q is quantized in its own launch
                 parts[qname + sfx] = byte_part(3 * nelem + 4 * nscale, kern[qname + sfx])
+    # end-to-end wrappers over the same FLOPs: FP8Linear.forward (activation quantizer or
+    # fused adaLN quantizer, LoRA down-projection, GEMM) and fp8_attention (quantizers +
+    # attention), from the per-part event times
+    lin_ms = sum(v for k, v in kern.items() if k.split("[")[0] in ("quant_rows", "adaln_quant", "lora_down", "gemm"))
+    att_ms = attn_ms + sum(v for k, v in kern.items() if k.startswith(("attn_quant", "attn_kmean")))
     step_flops = gemm_f + attn_f
     value = step_flops / (ms_step * 1e-3) / 1e12
     _, af, t_attn = biggest
@@ -423,6 +428,10 @@ def main() -> int:
         "frac_of_fp8_peak": round(value / PEAK_FP8_TFLOPS, 4),
         "gemm_tflops": round(gemm_f / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
         "attn_tflops": round(attn_f / (attn_ms * 1e-3) / 1e12, 1),
+        "end_to_end": {
+            "linear": {"ms": round(lin_ms, 4), "TFLOP/s": round(gemm_f / (lin_ms * 1e-3) / 1e12, 1)} if lin_ms else None,
+            "attention": {"ms": round(att_ms, 4), "TFLOP/s": round(attn_f / (att_ms * 1e-3) / 1e12, 1)},
+        },
         "roofline": {
             "kernel": f"{biggest[0]}: attn_fwd_kernel<128,...>",
             "bound": "mfma",

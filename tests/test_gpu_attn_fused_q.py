@@ -153,3 +153,30 @@ def test_fp8_attention_fused_and_two_call_paths_agree():
     v8t, sv = ops.attn_quant_v(vg)
     with pytest.raises(ValueError, match="unit channel stride"):
         ops.attn_fwd_q(q_odd, 1.0, k8, v8t, sk, sv, km, None, -1.0, S)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,masked", [(1, 20280, 20280, 0), (2, 21304, 21304, 384), (2, 21304, 512, 0)])
+def test_fused_q_full_size_equals_two_calls(B, Sq, Sk, masked):
+    """At the workloads' full sizes (480p self-attention, the joint self-attention with
+    item 1's last keys masked, text cross-attention), the fused launch and the two launches
+    give the same bits on every output element."""
+    _say(f"attn fused-Q full size B={B} Sq={Sq} Sk={Sk} masked={masked}")
+    from minimaxh3_amd import ops
+    H, D = 24, 128
+    g = torch.Generator(device="cuda").manual_seed(Sq + Sk)
+    q = torch.randn((B, Sq, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+    kv = torch.randn((B, Sk, 2, H, D), device="cuda", generator=g).to(torch.bfloat16)
+    k, v = kv[:, :, 0].permute(0, 2, 1, 3), kv[:, :, 1].permute(0, 2, 1, 3)
+    km = None
+    if masked:
+        km = torch.ones((B, Sk), dtype=torch.bool, device="cuda")
+        km[1, Sk - masked:] = False
+    c = ops.softmax_c(None, D)
+    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+    v8t, sv = ops.attn_quant_v(v)
+    q8, sq = ops.attn_quant_q(q, c)
+    two = ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, None, -1.0, q, Sk)
+    fused = ops.attn_fwd_q(q, c, k8, v8t, sk, sv, km, None, -1.0, Sk)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16))
+    assert torch.isfinite(fused.float()).all()

@@ -154,7 +154,9 @@ int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides[4],
  *   key_mask [B, Sk] uint8 (nonzero = keep) or NULL; key_bias [B, Sk] fp32 natural-log
  *   additive bias or NULL (entries <= -1e8 mask the key).
  *   out [B, H, Sq, D] of out_dtype (bf16/fp16) with element strides out_strides[4].
- *   Fully masked rows give 0.
+ *   Fully masked rows give 0.  Short key sequences (Sk <= 512 at D = 128, <= 1024 at
+ *   D = 64) without repair run a kernel that holds each head's K/V in LDS; same bits
+ *   (MXF8_ATTN_RESIDENT_KV=0 in the environment selects the streaming kernel).
  */
 int mxf8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t,
                   const float* sq, const float* sk, const float* sv,

@@ -32,6 +32,8 @@
 // products fetches its LDS fragments three products ahead.
 #pragma once
 
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace mxf8 {
@@ -158,15 +160,26 @@ struct AttnCtx {
   // attn_barrier.  Ends with a workgroup barrier.
   template <int QDT>
   __device__ __forceinline__ void quant_q(const AttnQ16& qa, int Sq, int nq, float* red) {
-    const int g = lane >> 5;
-    const bool valid = qrow < Sq;
-    const uint16_t* qp = qa.q + (int64_t)b * qa.sb + (int64_t)h * qa.sh + (int64_t)qrow * qa.ss + 32 * g;
     uint4 raw[D / 64][4];
+    load_q16(qa, b, h, qrow < Sq ? qrow : -1, lane, raw);
+    quant_q_raw<QDT>(raw, qa, nq, red);
+  }
+
+  // The 16-bit Q values this lane quantizes: row `row` of head (b_, h_), bytes
+  // [64 hh + 32 g, +32) of its codes; row < 0 loads nothing (zeros).
+  static __device__ __forceinline__ void load_q16(const AttnQ16& qa, int b_, int h_, int row, int lane_,
+                                                  uint4 (&raw)[D / 64][4]) {
+    const int g = lane_ >> 5;
+    const uint16_t* qp = qa.q + (int64_t)b_ * qa.sb + (int64_t)h_ * qa.sh + (int64_t)row * qa.ss + 32 * g;
 #pragma unroll
     for (int hh = 0; hh < D / 64; ++hh)
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        raw[hh][u] = valid ? *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u) : make_uint4(0, 0, 0, 0);
+        raw[hh][u] = row >= 0 ? *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u) : make_uint4(0, 0, 0, 0);
+  }
+
+  template <int QDT>
+  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], const AttnQ16& qa, int nq, float* red) {
     float f[D / 64][32];
     float amax = 0.0f;
 #pragma unroll
@@ -608,6 +621,9 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
   float l = st.lacc[0];
   if constexpr (DO_REPAIR) l += st.ldelta + __shfl_xor(st.ldelta, 32, 64);
   const float den = fmaxf(l, 1.0e-12f);
+  // (acc * sv) / den correctly rounded from one reciprocal per row (div_by_scale: the
+  // quotients are O's values and den lies in [1e-12, ~1e7], so nothing over- or underflows)
+  const float rden = __fdiv_rn(1.0f, den);
   const float* svh = sv + (int64_t)bh * D;
   char* obase = static_cast<char*>(out) + ((int64_t)b * os_b + (int64_t)h * os_h + (int64_t)qrow * os_s) * 2;
 #pragma unroll
@@ -621,7 +637,7 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
       for (int e = 0; e < 4; ++e) {
         float acc = st.o[dt][4 * q4 + e];
         if constexpr (DO_REPAIR) acc += st.orep[dt][4 * q4 + e];
-        const float v = __fdiv_rn(acc * sv4[e], den);
+        const float v = div_by_scale(acc * sv4[e], den, rden);
         ob[e] = ODT == MXF8_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
       }
       uint16_t* dst = reinterpret_cast<uint16_t*>(obase) + (int64_t)d0 * os_d;
@@ -703,12 +719,148 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
   attn_store<D, DO_REPAIR, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
 }
 
+// ---------------------------------------------------------------------------------------
+// Short key sequences (all KV tiles of a head fit in LDS: Sk <= 512 at D = 128, <= 1024 at
+// D = 64), Q from q8 / sq.  One persistent workgroup of 8 waves per CU walks a contiguous
+// range of (head, Q tile) work items; the head's K, V^T (and mask / bias) tiles are copied
+// into LDS once per head, and the two 4-wave groups take the range's Q tiles in pairs with
+// no barrier between heads.  Per Q tile the arithmetic and the KV visit order are those of
+// attn_fwd_kernel, so the output is the same bit for bit; what goes away is the per-tile
+// copy and barrier and the per-workgroup start-up, which dominate when a Q tile has only a
+// few KV tiles.  No repair path and no fused Q quantizer (its block amax would hold the two
+// groups in lockstep): the launcher uses attn_fwd_kernel for those.
+// ---------------------------------------------------------------------------------------
+template <int D>
+struct AttnResident {
+  static constexpr int NKMAX = D == 128 ? 4 : 8;  // KV tiles held in LDS
+};
+
+template <int D, bool HAS_MASK, bool HAS_BIAS, int ODT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8,
+                              const uint8_t* __restrict__ v8t, const float* __restrict__ sq,
+                              const float* __restrict__ sk, const float* __restrict__ sv,
+                              const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias,
+                              void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H,
+                              int Sq, int Sk, int nq, int total) {
+  typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
+  constexpr int NKMAX = AttnResident<D>::NKMAX;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NKMAX * T::BUF];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
+  const int nk = (Sk + 127) / 128;
+  const AttnFragOfs<D> fo(lane);
+  const int ta = (int)(((int64_t)blockIdx.x * total) / gridDim.x);
+  const int tb = (int)(((int64_t)(blockIdx.x + 1) * total) / gridDim.x);
+  // Work item of this wave's group in the pair that starts at tile p: active when that
+  // tile exists (p + grp < end of p's head segment), else a stand-in id.
+  auto pair_item = [&](int p, bool& active) {
+    const int seg_end = min(tb, (p / nq + 1) * nq);
+    active = p + grp < seg_end;
+    return active ? p + grp : p;
+  };
+  // The next tile's Q fragments and scale are fetched before the current tile's output
+  // stores: loads and stores retire in order, so a load issued after the stores would wait
+  // for them to reach memory.
+  v8i qnext[D / 64];
+  float sqnext = 0.0f;
+  auto fetch_q = [&](int id) {
+    const int bh_ = id / nq, I_ = id - bh_ * nq;
+    const int row = I_ * 128 + wq * 32 + (lane & 31);
+    const uint8_t* qp = q8 + ((int64_t)bh_ * nq * 128 + row) * D + 32 * (lane >> 5);
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh) {
+      const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
+      const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
+      qnext[hh] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    sqnext = sq[(int64_t)bh_ * nq + I_];
+  };
+  int loaded = -1;
+  int p = ta;
+  if (p < tb) {
+    bool act;
+    fetch_q(pair_item(p, act));
+  }
+  while (p < tb) {
+    const int bh = p / nq;
+    const int seg_end = min(tb, (bh + 1) * nq);
+    if (bh != loaded) {
+      // every wave is done with the previous head's tiles
+      attn_barrier();
+      const AttnCtx<D, HAS_MASK, HAS_BIAS, true> dc(nullptr, k8, v8t, nullptr, sk, key_mask, key_bias, H, Sk, nq,
+                                                    bh * nq, wq, lane);
+      for (int j = grp; j < nk; j += 2) {
+        uint8_t* buf = smem + j * T::BUF;
+        dc.dma_k(buf, j * 128);
+        dc.dma_v(buf + T::KB, j * 128);
+        dc.dma_aux(buf + T::KB + T::VB, j * 128, Sk);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      attn_barrier();
+      loaded = bh;
+    }
+    bool active;
+    const int id = pair_item(p, active);
+    AttnCtx<D, HAS_MASK, HAS_BIAS, true> cx(nullptr, k8, v8t, nullptr, sk, key_mask, key_bias, H, Sk, nq, id, wq,
+                                            lane);
+#pragma unroll
+    for (int hh = 0; hh < D / 64; ++hh) cx.qf[hh] = qnext[hh];
+    cx.sqI = sqnext;
+    const int np = p + 2 < seg_end ? p + 2 : seg_end;  // first tile of the next pair
+    AttnState<D, false> st;
+    if (active) {
+      st.init();
+      int j = (int)(((int64_t)cx.I * nk) / nq);
+      for (int i = 0; i < nk; ++i) {
+        const uint8_t* buf = smem + j * T::BUF;
+        const float skj = cx.skh[j];
+        const int kv0 = j * 128;
+        v16f s[4];
+        v8i pf[2];
+        AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+        if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
+          attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
+        const float m_new = attn_codes<HAS_BIAS>(s, cx.sqI, skj, st.m, pf);
+        if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
+        st.m = m_new;
+        AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+        j = j + 1 == nk ? 0 : j + 1;
+      }
+    }
+    if (np < tb) {
+      bool nact;
+      fetch_q(pair_item(np, nact));
+    }
+    if (active && cx.qrow < Sq)
+      attn_store<D, false, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+    p = np;
+  }
+}
+
+// Whether the resident-KV kernel may take a launch: MXF8_ATTN_RESIDENT_KV=0 in the
+// environment turns it off (read at every launch, so a process can compare both kernels).
+inline bool attn_resident_enabled() {
+  const char* e = getenv("MXF8_ATTN_RESIDENT_KV");
+  return !(e != nullptr && e[0] == '0');
+}
+
 template <int D, bool M_, bool B_, bool R_, int ODT>
 static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t, const float* sq, const float* sk,
                         const float* sv, const uint8_t* km, const float* kb, float tau, void* out,
                         const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa,
                         hipStream_t st) {
   const int64_t nq = cdiv(Sq, 128);
+  const int64_t nk = cdiv(Sk, 128);
+  const int64_t total = nq * B * H;
+  if (!R_ && qa == nullptr && nk <= AttnResident<D>::NKMAX && attn_resident_enabled()) {
+    const int cus = device_cus();
+    const unsigned g = (unsigned)(cus > 0 && total > cus ? cus : total);
+    attn_fwd_resident_kernel<D, M_, B_, ODT><<<dim3(g), 512, 0, st>>>(
+        q8, k8, v8t, sq, sk, sv, km, kb, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
+        (int)total);
+    return;
+  }
   const dim3 grid((unsigned)(nq * B * H));
   if (qa != nullptr)
     attn_fwd_kernel<D, M_, B_, R_, ODT, true><<<grid, 256, 0, st>>>(

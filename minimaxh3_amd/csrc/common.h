@@ -24,6 +24,20 @@ constexpr float kScaleFloor = 1.0e-12f;
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device; 0 if the query fails).
+inline int device_cus() {
+  constexpr int kMaxDev = 64;
+  static int cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  int n = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    __atomic_store_n(&cache[dev], n, __ATOMIC_RELAXED);
+  }
+  return n;
+}
+
 // ---- scalar conversions ---------------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 

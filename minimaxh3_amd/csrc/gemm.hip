@@ -558,19 +558,6 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restric
     }
 }
 
-// Compute units of the current device (cached per device; 0 if the query fails).
-static int device_cus() {
-  constexpr int kMaxDev = 64;
-  static int cache[kMaxDev];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-  int n = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    __atomic_store_n(&cache[dev], n, __ATOMIC_RELAXED);
-  }
-  return n;
-}
 
 template <class C, int ACT, int LM, bool KTAIL>
 static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,

@@ -1,0 +1,107 @@
+"""GPU parity of the resident-KV attention kernel (short key sequences).
+
+When every KV tile of a head fits in LDS (Sk <= 512 at D = 128, <= 1024 at D = 64), Q comes
+from q8 / sq (mxf8_attn_fwd) and no repair is asked for, the launcher runs
+attn_fwd_resident_kernel.  Per Q tile it performs
+attn_fwd_kernel's arithmetic in the same KV visit order, so both kernels must give the same
+bits; MXF8_ATTN_RESIDENT_KV=0 selects attn_fwd_kernel for the comparison.  The output is
+also held to the attention bar against the oracle.
+"""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from tests.helpers import assert_attn_close, bf16_randn, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _both(fn):
+    """fn() with the resident kernel allowed, then with it switched off."""
+    saved = os.environ.get("MXF8_ATTN_RESIDENT_KV")
+    try:
+        os.environ.pop("MXF8_ATTN_RESIDENT_KV", None)
+        a = fn()
+        os.environ["MXF8_ATTN_RESIDENT_KV"] = "0"
+        b = fn()
+    finally:
+        if saved is None:
+            os.environ.pop("MXF8_ATTN_RESIDENT_KV", None)
+        else:
+            os.environ["MXF8_ATTN_RESIDENT_KV"] = saved
+    torch.cuda.synchronize()
+    return a, b
+
+
+CASES = [
+    # B, H, Sq, Sk, D, dtype, mask, bias
+    (2, 3, 1000, 512, 128, torch.bfloat16, False, False),
+    (1, 5, 700, 300, 128, torch.bfloat16, True, False),
+    (2, 2, 257, 77, 128, torch.float16, False, True),
+    (2, 2, 390, 500, 128, torch.bfloat16, True, True),
+    (1, 4, 333, 1024, 64, torch.bfloat16, True, False),
+    (3, 2, 129, 900, 64, torch.float16, False, True),
+    (1, 1, 5, 128, 128, torch.bfloat16, False, False),
+    (1, 3, 640, 256, 64, torch.bfloat16, True, True),
+]
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D,dtype,use_mask,use_bias", CASES)
+def test_resident_kv_equals_streaming_kernel(B, H, Sq, Sk, D, dtype, use_mask, use_bias):
+    _say(f"attn resident-KV B={B} H={H} Sq={Sq} Sk={Sk} D={D} {dtype} mask={use_mask} bias={use_bias}")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(Sq * 7 + Sk * 3 + D)
+    q = bf16_randn(rng, (B, H, Sq, D))
+    k, v = bf16_randn(rng, (B, H, Sk, D)), bf16_randn(rng, (B, H, Sk, D))
+    if dtype == torch.float16:
+        q, k, v = (t.astype(np.float16).astype(np.float32) for t in (q, k, v))
+    mask = bias = None
+    if use_mask:
+        mask = np.ones((B, Sk), bool)
+        mask[-1, Sk // 3:] = False
+        mask[0, rng.choice(Sk, Sk // 8, replace=False)] = False
+    if use_bias:
+        bias = (rng.standard_normal((B, Sk)) * 0.5).astype(np.float32)
+        bias[0, :5] = -1e9
+    qg = to_gpu(np.ascontiguousarray(q.transpose(0, 2, 1, 3)), dtype).permute(0, 2, 1, 3)
+    kg, vg = to_gpu(k, dtype), to_gpu(v, dtype)
+    km = None if mask is None else to_gpu(mask.astype(np.uint8), torch.bool)
+    kb = None if bias is None else to_gpu(bias, torch.float32)
+    c = np.float32(oa.LOG2E / math.sqrt(D))
+    k8, sk = ops.attn_quant_k(kg, ops.attn_kmean(kg))
+    v8t, sv = ops.attn_quant_v(vg)
+    q8, sq = ops.attn_quant_q(qg, float(c))
+    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, qg, Sk))
+    assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    ref, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=-1.0,
+                              out_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
+    assert_attn_close(res.float().cpu().numpy(), ref)
+
+
+def test_resident_kv_text_cross_attention_full_size():
+    """The joint workload's text cross-attention (B=2, H=24, Sq=21304, Sk=512): both kernels
+    give the same bits at full size."""
+    _say("attn resident-KV full-size cross-attention")
+    from minimaxh3_amd import ops
+    B, H, Sq, Sk, D = 2, 24, 21304, 512, 128
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn((B, Sq, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+    kv = torch.randn((B, Sk, 2, H, D), device="cuda", generator=g).to(torch.bfloat16)
+    k, v = kv[:, :, 0].permute(0, 2, 1, 3), kv[:, :, 1].permute(0, 2, 1, 3)
+    c = ops.softmax_c(None, D)
+    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+    v8t, sv = ops.attn_quant_v(v)
+    q8, sq = ops.attn_quant_q(q, c)
+    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, Sk))
+    assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    assert torch.isfinite(res.float()).all()

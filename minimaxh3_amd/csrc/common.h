@@ -85,9 +85,11 @@ __device__ __forceinline__ float e4m3_scale(float amax) {
 // x - s q0 is exact with an fma, and RN(q0 + rem * r) is RN(x / s) (Markstein's
 // theorem, binary fp32, no overflow; quotients here are bounded by ~448).  The sign is
 // copied back because for x = -0 the remainder step yields +0 (IEEE -0 / s is -0).
+// For s = +inf (a block maximum of inf) r is 0: with s capped at the largest finite value
+// in the remainder step, a finite x gives +-0 (IEEE x / inf) and +-inf or NaN gives NaN.
 __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
   float q0 = x * r;
-  float rem = __builtin_fmaf(-q0, s, x);
+  float rem = __builtin_fmaf(-q0, fminf(s, 3.40282347e38f), x);
   return __builtin_copysignf(__builtin_fmaf(rem, r, q0), x);
 }
 

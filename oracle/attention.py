@@ -20,7 +20,7 @@ import math
 
 import numpy as np
 
-from .numerics import E4M3_MAX, bf16_round, e4m3_decode, e4m3_encode
+from .numerics import E4M3_MAX, absmax_maxnum, bf16_round, clamp448_maxnum, e4m3_decode, e4m3_encode
 
 F32 = np.float32
 LOG2E = 1.4426950408889634
@@ -43,11 +43,11 @@ def _blockwise_quant(t, valid_rows, block):
     pad = nb * block - S
     tp = np.concatenate([t, np.zeros((B, H, pad, D), F32)], axis=2) if pad else t
     tb = tp.reshape(B, H, nb, block, D)
-    amax = np.max(np.abs(tb), axis=(3, 4))
-    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
-    q = (tb / scale[..., None, None]).astype(F32)
-    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
-    codes = e4m3_encode(q).reshape(B, H, nb * block, D)[:, :, :S]
+    amax = absmax_maxnum(tb, axis=(3, 4))
+    scale = (np.fmax(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    with np.errstate(invalid="ignore"):  # inf / inf -> NaN, clamped below
+        q = (tb / scale[..., None, None]).astype(F32)
+    codes = e4m3_encode(clamp448_maxnum(q)).reshape(B, H, nb * block, D)[:, :, :S]
     return codes, scale
 
 
@@ -82,10 +82,11 @@ def quantize_v(v):
     Returns (V8T uint8 [B,H,D,Sk], sV fp32 [B,H,D]).
     """
     v = np.asarray(v, F32)
-    amax = np.max(np.abs(v), axis=2)
-    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
-    q = (v / scale[:, :, None, :]).astype(F32)
-    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
+    amax = absmax_maxnum(v, axis=2)
+    scale = (np.fmax(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    with np.errstate(invalid="ignore"):  # inf / inf -> NaN, clamped below
+        q = (v / scale[:, :, None, :]).astype(F32)
+    q = clamp448_maxnum(q)
     return np.ascontiguousarray(e4m3_encode(q).transpose(0, 1, 3, 2)), scale
 
 

@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .numerics import E4M3_MAX, bf16_round, e4m3_decode, e4m3_encode
+from .numerics import E4M3_MAX, absmax_maxnum, bf16_round, clamp448_maxnum, e4m3_decode, e4m3_encode
 
 F32 = np.float32
 
@@ -35,11 +35,11 @@ def quantize_rows(x):
     M, K = x.shape
     if K == 0:
         return np.zeros((M, 0), np.uint8), np.full((M, 1), F32(1e-12) / F32(E4M3_MAX), F32)
-    amax = np.max(np.abs(x), axis=1)
-    scale = (np.maximum(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
-    q = (x / scale[:, None]).astype(F32)
-    q = np.minimum(np.maximum(q, F32(-E4M3_MAX)), F32(E4M3_MAX))
-    return e4m3_encode(q), scale.reshape(M, 1)
+    amax = absmax_maxnum(x, axis=1)
+    scale = (np.fmax(amax, F32(1e-12)) / F32(E4M3_MAX)).astype(F32)
+    with np.errstate(invalid="ignore"):  # inf / inf -> NaN, clamped below
+        q = (x / scale[:, None]).astype(F32)
+    return e4m3_encode(clamp448_maxnum(q)), scale.reshape(M, 1)
 
 
 def scaled_mm(x8, w8, sa, sw, bias=None):

@@ -20,6 +20,19 @@ _MIN_NORMAL = 2.0 ** -6     # smallest normal e4m3 value (code 0x08)
 _SUB_STEP = 2.0 ** -9       # spacing of e4m3 subnormals
 
 
+def absmax_maxnum(x, axis) -> np.ndarray:
+    """max |x| over `axis` with IEEE maxNum semantics: NaN elements are skipped (all-NaN
+    gives NaN).  The reference's Triton `tl.max` / `tl.maximum` (default: no NaN
+    propagation; `max.f32` on its GPUs) behave so (kernels/fp8_linear.py:20-21)."""
+    return np.fmax.reduce(np.abs(np.asarray(x, np.float32)), axis=axis)
+
+
+def clamp448_maxnum(q) -> np.ndarray:
+    """`tl.minimum(tl.maximum(q, -448), 448)` (kernels/fp8_linear.py:22) with maxNum /
+    minNum semantics: a NaN quotient becomes -448."""
+    return np.fmin(np.fmax(q, np.float32(-E4M3_MAX)), np.float32(E4M3_MAX))
+
+
 def e4m3_encode(x) -> np.ndarray:
     """Round fp32 values to e4m3fn codes (uint8), round-to-nearest-even.
 

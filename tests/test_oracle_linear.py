@@ -151,3 +151,23 @@ def test_adaln_modulate_matches_torch_ops():
     ye = adaln_modulate(x.reshape(B * S, C), shift, scale, S, eps=eps, eager=True)
     yf = adaln_modulate(x.reshape(B * S, C), shift, scale, S, eps=eps, eager=False)
     assert (ye != yf).mean() > 0.01
+
+
+def test_quantize_rows_non_finite_follow_the_reference_clamp():
+    """Closed forms for non-finite rows under the reference's Triton semantics
+    (kernels/fp8_linear.py:20-22: tl.max / tl.maximum / tl.minimum skip NaN): a NaN does
+    not enter the row maximum and its quotient clamps to -448 (0xFE); a row maximum of inf
+    gives the scale inf, finite elements x / inf = +-0 (0x00 / 0x80), +-inf -> NaN -> -448."""
+    inf, nan = np.inf, np.nan
+    x = np.array([[inf, 1.0, -2.0, 0.0],
+                  [nan, 448.0, -224.0, 1.0],
+                  [nan, nan, nan, nan],
+                  [-inf, 5.0, -0.0, nan]], np.float32)
+    codes, scale = quantize_rows(x)
+    assert scale[0, 0] == inf and scale[3, 0] == inf
+    assert scale[1, 0] == np.float32(1.0)
+    assert scale[2, 0] == np.float32(np.float32(1e-12) / np.float32(448.0))
+    np.testing.assert_array_equal(codes, np.array([[0xFE, 0x00, 0x80, 0x00],
+                                                   [0xFE, 0x7E, 0xF6, 0x38],
+                                                   [0xFE, 0xFE, 0xFE, 0xFE],
+                                                   [0xFE, 0x00, 0x80, 0xFE]], np.uint8))

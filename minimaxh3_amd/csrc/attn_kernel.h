@@ -291,7 +291,9 @@ struct AttnState {
   static constexpr int NDT = D / 32;  // O^T row tiles
   v16f o[NDT];
   v16f orep[DO_REPAIR ? NDT : 1];
-  v16f lacc;     // every register holds the running sum of P codes of the lane's query
+  // Running sums of the P codes from the 16x16x128 row-sum product: lane n < 16 holds query
+  // n's in register 0 and query n + 16's in register 1 (see AttnMfmaRun, x == NDT).
+  v4f lacc;
   float m;       // lazy row max (log2 domain)
   float ldelta;  // repair: running sum of the exact-minus-code corrections (lane's keys)
 
@@ -304,7 +306,7 @@ struct AttnState {
         if constexpr (DO_REPAIR) orep[dt][i] = 0.0f;
       }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+    for (int i = 0; i < 4; ++i) lacc[i] = 0.0f;
     m = kAttnNeg;
     ldelta = 0.0f;
   }
@@ -320,8 +322,10 @@ struct AttnState {
         for (int i = 0; i < 16; ++i) orep[dt][i] *= alpha;
       }
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) lacc[i] *= alpha;
+    // register 1 of lane n holds query n + 16's sum: it takes that query's alpha
+    const float alpha16 = __shfl(alpha, ((int)(__lane_id() & 15)) + 16, 64);
+    lacc[0] *= alpha;
+    lacc[1] *= alpha16;
     if constexpr (DO_REPAIR) ldelta *= alpha;
   }
 };
@@ -338,8 +342,20 @@ template <int D>
 struct AttnFragOfs {
   int k[D / 64][2];  // K tile: half hh, chunk 4 hh + 2 g + e
   int v[2][2];       // V^T tile: key half kh, chunk 4 kh + 2 g + e
+  // A operand of the 16x16x128 row-sum product over one 64-key half of P.  As its B
+  // operand, the PV fragment of lane l holds 32 codes of query l % 32; the product reads
+  // lane n + 16 j as column n, k range [32 j, +32), i.e. query n for j = 0, 2 and query
+  // n + 16 for j = 1, 3.  Row 0 of A is 1.0 (e4m3 0x38) on k groups 0 and 2, row 1 on
+  // groups 1 and 3, other rows 0: output row 0 is query n's sum, row 1 query n + 16's.
+  v8i rowsum_sel;
   __device__ __forceinline__ explicit AttnFragOfs(int lane) {
     const int r = lane & 31, g = lane >> 5;
+    {
+      const int row = lane & 15, j = lane >> 4;
+      const bool one = (row == 0 && (j & 1) == 0) || (row == 1 && (j & 1) == 1);
+      const int w = one ? 0x38383838 : 0;
+      rowsum_sel = v8i{w, w, w, w, w, w, w, w};
+    }
 #pragma unroll
     for (int hh = 0; hh < D / 64; ++hh)
 #pragma unroll
@@ -376,7 +392,7 @@ struct AttnMfmaRun {
     if constexpr (K < NPV) {
       constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
       if constexpr (x == NDT)
-        return v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+        return fo.rowsum_sel;
       else
         return lds_pair(sV + x * 32 * 128, fo.v[kh][0], fo.v[kh][1]);
     } else {
@@ -391,7 +407,7 @@ struct AttnMfmaRun {
     if constexpr (K < NPV) {
       constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
       if constexpr (x == NDT)
-        st.lacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
+        st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
       else
         st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pf[kh], st.o[x], 0, 0, 0, 0, 0, 0);
     } else {
@@ -618,7 +634,10 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
                                            int64_t os_d) {
   constexpr int NDT = D / 32;
   const int g = lane >> 5;
-  float l = st.lacc[0];
+  // row sum of this lane's query q = lane % 32: register q / 16 of lane q % 16
+  const int q = lane & 31;
+  const float l0 = __shfl(st.lacc[0], q & 15, 64), l1 = __shfl(st.lacc[1], q & 15, 64);
+  float l = q < 16 ? l0 : l1;
   if constexpr (DO_REPAIR) l += st.ldelta + __shfl_xor(st.ldelta, 32, 64);
   const float den = fmaxf(l, 1.0e-12f);
   // (acc * sv) / den correctly rounded from one reciprocal per row (div_by_scale: the

@@ -105,3 +105,28 @@ def test_resident_kv_text_cross_attention_full_size():
     res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, Sk))
     assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
     assert torch.isfinite(res.float()).all()
+
+
+@pytest.mark.parametrize("D,Sk", [(128, 300), (64, 1000)])
+def test_resident_kv_many_tiles_per_workgroup_mask_bias(D, Sk):
+    """More Q tiles than CUs (B=2, H=8, Sq=21000: 2640 work items), so each workgroup walks a
+    range that crosses heads at arbitrary offsets and pairs tiles; with a key mask, a bias and
+    a ragged last key tile.  Bit for bit against the streaming kernel."""
+    _say(f"attn resident-KV many tiles D={D} Sk={Sk}")
+    from minimaxh3_amd import ops
+    B, H, Sq = 2, 8, 21000
+    g = torch.Generator(device="cuda").manual_seed(D + Sk)
+    q = torch.randn((B, Sq, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+    kv = torch.randn((B, Sk, 2, H, D), device="cuda", generator=g).to(torch.bfloat16)
+    k, v = kv[:, :, 0].permute(0, 2, 1, 3), kv[:, :, 1].permute(0, 2, 1, 3)
+    km = torch.rand((B, Sk), device="cuda", generator=g) > 0.25
+    km[1, Sk // 2:] = False
+    kb = torch.randn((B, Sk), device="cuda", generator=g)
+    kb[0, :4] = -1e9
+    c = ops.softmax_c(None, D)
+    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+    v8t, sv = ops.attn_quant_v(v)
+    q8, sq = ops.attn_quant_q(q, c)
+    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, q, Sk))
+    assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    assert torch.isfinite(res.float()).all()

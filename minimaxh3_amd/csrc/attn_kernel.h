@@ -16,8 +16,9 @@
 // accumulator registers, packed 4 codes per dword, ARE the B operand of the PV MFMA
 // (O^T = V^T P^T) with V^T read as contiguous 32-byte runs of a v8t row: no cross-lane
 // shuffles between the two products.  The row sums l come from the matrix cores too: one
-// more MFMA per 64 keys with an all-ones A operand.  K and V^T tiles (and the mask / bias
-// of the tile) are copied global -> LDS by the direct-to-LDS DMA.
+// v_mfma_f32_16x16x128_f8f6f4 per 64 keys that reads the P fragment as its B operand and
+// a lane-constant 0/1 selector as A (AttnFragOfs::rowsum_sel).  K and V^T tiles (and the
+// mask / bias of the tile) are copied global -> LDS by the direct-to-LDS DMA.
 //
 // Per score the VALU does half a 3-input max and three FMAs (8 S + 56 - 8 m straight from
 // the fp32 dot product with the per-tile constant 8 sq sk; the flush test as a clamped FMA;
@@ -424,12 +425,12 @@ struct AttnMfmaRun {
   }
 
   template <int K, bool REP>
-  __device__ static __forceinline__ void seq(v8i (&fr)[4], const uint8_t* sV, const uint8_t* sK,
+  __device__ static __forceinline__ void seq(v8i (&fr)[RING], const uint8_t* sV, const uint8_t* sK,
                                              const AttnFragOfs<D>& fo, const v8i (&pf)[2], const v8i (&qf)[D / 64],
                                              v16f (&s)[4], AttnState<D, REP>& st) {
     if constexpr (K < N) {
-      if constexpr (K + 3 < N) fr[(K + 3) & 3] = frag<K + 3>(sV, sK, fo);
-      exec<K, REP>(fr[K & 3], pf, qf, s, st);
+      if constexpr (K + AHEAD < N) fr[(K + AHEAD) % RING] = frag<K + AHEAD>(sV, sK, fo);
+      exec<K, REP>(fr[K % RING], pf, qf, s, st);
       // keep program order: a reordered run would hold the scores and the PV fragments
       // live together
       __builtin_amdgcn_sched_barrier(0);
@@ -437,14 +438,22 @@ struct AttnMfmaRun {
     }
   }
 
+  // the first AHEAD fragments of the run
+  template <int K>
+  __device__ static __forceinline__ void prime(v8i (&fr)[RING], const uint8_t* sV, const uint8_t* sK,
+                                               const AttnFragOfs<D>& fo) {
+    if constexpr (K < AHEAD && K < N) {
+      fr[K] = frag<K>(sV, sK, fo);
+      prime<K + 1>(fr, sV, sK, fo);
+    }
+  }
+
   template <bool REP>
   __device__ static __forceinline__ void run(const uint8_t* sV, const uint8_t* sK, const AttnFragOfs<D>& fo,
                                              const v8i (&pf)[2], const v8i (&qf)[D / 64], v16f (&s)[4],
                                              AttnState<D, REP>& st) {
-    v8i fr[4];
-    fr[0] = frag<0>(sV, sK, fo);
-    if constexpr (N > 1) fr[1] = frag<1>(sV, sK, fo);
-    if constexpr (N > 2) fr[2] = frag<2>(sV, sK, fo);
+    v8i fr[RING];
+    prime<0>(fr, sV, sK, fo);
     seq<0, REP>(fr, sV, sK, fo, pf, qf, s, st);
   }
 };

@@ -1,0 +1,26 @@
+"""bench.py's command-line contract that needs no GPU: one GPU only, and its flags parse."""
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                          timeout=300, cwd=ROOT)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = _run("--gpus", "2")
+    assert r.returncode != 0
+    assert "--gpus 2 is not supported" in r.stderr
+
+
+def test_help_lists_the_workloads_and_switches():
+    r = _run("--help")
+    assert r.returncode == 0
+    for flag in ("--steps", "--warmup", "--workload", "--no-cpu-baseline", "--separate-q-quant"):
+        assert flag in r.stdout
+    for workload in ("dit480", "joint", "dit720"):
+        assert workload in r.stdout

@@ -35,7 +35,7 @@ reference's torch CPU fallbacks (fp32 dequant-matmul and SDPA) on a bounded samp
 scales those rates to the step's FLOP mix.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload dit480|joint|dit720]
-                    [--no-cpu-baseline] [--separate-q-quant]
+                    [--no-cpu-baseline] [--separate-q-quant] [--repair-tau TAU]
 """
 from __future__ import annotations
 
@@ -171,8 +171,9 @@ class Timers:
         return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
 
 
-def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True):
-    """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make."""
+def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True, tau: float = -1.0):
+    """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make
+    (tau: the attention's repair threshold, < 0 for none)."""
     tick = timers.start if timers else (lambda n: None)
     tock = timers.stop if timers else (lambda t: None)
     outs = []
@@ -208,14 +209,14 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bo
         if fuse_q:
             # the Q quantizer runs inside the attention launch
             t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, -1.0, k.shape[2]))
+            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, tau, k.shape[2]))
             tock(t)
         else:
             t = tick("attn_quant_q" + sfx)
             q8, sq = ops.attn_quant_q(q, c)
             tock(t)
             t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, -1.0, q, k.shape[2]))
+            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, tau, q, k.shape[2]))
             tock(t)
     return outs
 
@@ -244,9 +245,24 @@ def hbm_stream_reference(torch, dev, mib: int = 1024, reps: int = 5) -> dict:
             "ms": round(ms, 4), "GB/s": round(2 * mib * (1 << 20) / ms / 1e6, 1)}
 
 
-def cpu_baseline(step_lin: float, step_att: float, target_s: float = 12.0) -> dict:
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(step_lin: float, step_att: float, runs: int = 5) -> dict:
     """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix
-    (step_lin GEMM FLOPs, step_att attention FLOPs)."""
+    (step_lin GEMM FLOPs, step_att attention FLOPs): the median of `runs` timed runs of each
+    part after one warmup run."""
+    import statistics
+
     import torch
 
     from oracle.cpu_baseline import dequant_linear, quantize_rows_torch, sdpa_fallback
@@ -254,7 +270,7 @@ def cpu_baseline(step_lin: float, step_att: float, target_s: float = 12.0) -> di
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    ms = 512
+    ms = 2048
     lin = []
     for _, k, n, _ in LINEARS:
         x = torch.randn((ms, k), generator=g).to(torch.bfloat16)
@@ -263,23 +279,22 @@ def cpu_baseline(step_lin: float, step_att: float, target_s: float = 12.0) -> di
         w8, sw = quantize_rows_torch(w)
         lin.append((x8, sa, w8, sw.view(1, -1), (torch.randn((n,), generator=g) * 0.01).to(torch.bfloat16)))
     lin_flops = sum(gemm_flops(ms, n, k) for _, k, n, _ in LINEARS)
-    hs = 1
+    hs = 2
     q, k, v = (torch.randn((1, hs, TOKENS, HEAD_DIM), generator=g) for _ in range(3))
     at_flops = attn_flops(1, hs, TOKENS, TOKENS, HEAD_DIM)
 
-    def timed(fn, budget):
+    def median_time(fn):
         fn()  # warmup
-        reps, t0 = 0, time.perf_counter()
-        while True:
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
             fn()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget or reps >= 50:
-                return el / reps
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
 
     # the linear sample is skipped for a workload without linears
-    t_lin = timed(lambda: [dequant_linear(*a) for a in lin], target_s / 2) if step_lin else float("inf")
-    t_att = timed(lambda: sdpa_fallback(q, k, v), target_s / 2)
+    t_lin = median_time(lambda: [dequant_linear(*a) for a in lin]) if step_lin else float("inf")
+    t_att = median_time(lambda: sdpa_fallback(q, k, v))
     lin_rate, att_rate = lin_flops / t_lin, at_flops / t_att
     step_s = (step_lin / lin_rate if step_lin else 0.0) + step_att / att_rate
     return {
@@ -287,10 +302,10 @@ def cpu_baseline(step_lin: float, step_att: float, target_s: float = 12.0) -> di
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"torch CPU fp32 dequant-matmul of the 4 DiT linears on {ms} of {TOKENS} tokens "
-                   f"({lin_rate / 1e12:.3f} TFLOP/s) and fp32 SDPA on {hs} of {HEADS} heads at S={TOKENS} "
-                   f"({att_rate / 1e12:.3f} TFLOP/s); value = the step's FLOPs over the step time these "
-                   f"rates imply ({step_s:.1f} s); host {platform.processor() or platform.machine()}, "
+        "sample": (f"median of {runs} runs after a warmup: torch CPU fp32 dequant-matmul of the 4 DiT linears on "
+                   f"{ms} of {TOKENS} tokens ({lin_rate / 1e12:.3f} TFLOP/s) and fp32 SDPA on {hs} of {HEADS} heads "
+                   f"at S={TOKENS} ({att_rate / 1e12:.3f} TFLOP/s); value = the step's FLOPs over the step time "
+                   f"these rates imply ({step_s:.1f} s, heads scaled x{HEADS // hs}); host {cpu_model()}, "
                    f"{cores} threads"),
     }
 
@@ -304,6 +319,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--separate-q-quant", action="store_true",
                     help="quantize Q in its own launch instead of inside the attention launch")
+    ap.add_argument("--repair-tau", type=float, default=-1.0,
+                    help="exact repair of P codes >= tau in every attention (the reference's quality "
+                         "profile uses 0.5); < 0 disables it (default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "
@@ -323,6 +341,7 @@ def main() -> int:
     _native.require_gfx950(dev)
     desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]
     fuse_q = not args.separate_q_quant
+    tau = float(args.repair_tau)
     log("[bench] HBM streaming reference")
     stream_ref = hbm_stream_reference(torch, dev)
     log(f"[bench] building workload {args.workload}")
@@ -331,7 +350,7 @@ def main() -> int:
 
     with torch.inference_mode():
         for i in range(args.warmup):
-            run_step(torch, ops, linears, attn_inputs, None, fuse_q)
+            run_step(torch, ops, linears, attn_inputs, None, fuse_q, tau)
         torch.cuda.synchronize()
         log(f"[bench] warmup done ({args.warmup} steps)")
         # The timed steps bracket only the attention launches (the roofline kernel) with HIP
@@ -340,14 +359,14 @@ def main() -> int:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, roof_timers, fuse_q)
+            run_step(torch, ops, linears, attn_inputs, roof_timers, fuse_q, tau)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
         # per-launch breakdown: the same steps again, every launch bracketed (not timed)
         timers = Timers(torch)
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, timers, fuse_q)
+            run_step(torch, ops, linears, attn_inputs, timers, fuse_q, tau)
         torch.cuda.synchronize()
     ms_step = elapsed * 1e3 / args.steps
     kern = timers.mean_ms()
@@ -423,6 +442,7 @@ def main() -> int:
             "workload": desc,
             "tokens": tokens or None, "hidden": HIDDEN, "mlp": MLP, "heads": HEADS, "head_dim": HEAD_DIM,
             "lora_rank": lora_rank or None,
+            "repair_tau": tau if tau >= 0 else None,
             "step_tflop": round(step_flops / 1e12, 4),
         },
         "frac_of_fp8_peak": round(value / PEAK_FP8_TFLOPS, 4),

@@ -27,10 +27,16 @@
 // twice; the row max that drives the lazy-max policy is still computed exactly as
 // (max * sq) * sk.
 //
-// One workgroup per Q tile processes one KV tile at a time: S = QK^T, codes, PV (plus the
-// repair).  Two workgroups share a CU (without repair the kernel fits 256 VGPRs), so one
-// wave's softmax overlaps the other's matrix products on each SIMD.  Each run of matrix
-// products fetches its LDS fragments three products ahead.
+// The repair correction delta = exp2(S - m) - P (where P >= tau) is formed from the same
+// bits and split into two e4m3 parts of 8 delta that the PV products multiply with the V^T
+// fragments already loaded for P V, at the MFMA's E8M0 block scale 2^-3; their row sums
+// join l on the row-sum product.  The corrections accumulate into O itself (the reference
+// keeps them in a second accumulator and adds the two at the end).
+//
+// One workgroup per Q tile processes one KV tile at a time: S = QK^T, codes, PV.  Two
+// workgroups share a CU (the kernel fits 256 registers), so one wave's softmax overlaps
+// the other's matrix products on each SIMD.  Each run of matrix products fetches its LDS
+// fragments three products ahead.
 #pragma once
 
 #include <stdlib.h>
@@ -287,54 +293,41 @@ struct AttnCtx {
   }
 };
 
-template <int D, bool DO_REPAIR>
+// Running state of a wave's 32 queries.  With the repair, the corrections go into the same
+// accumulators: O and O_r (and the two parts of l) are scaled by the same factors and only
+// their sum is used, so one set holds both (fp32 summation order is all that changes).
+template <int D>
 struct AttnState {
   static constexpr int NDT = D / 32;  // O^T row tiles
   v16f o[NDT];
-  v16f orep[DO_REPAIR ? NDT : 1];
-  // Running sums of the P codes from the 16x16x128 row-sum product: lane n < 16 holds query
-  // n's in register 0 and query n + 16's in register 1 (see AttnMfmaRun, x == NDT).
+  // Running sums of the P codes (and repair corrections) from the 16x16x128 row-sum
+  // product: lane n < 16 holds query n's in register 0 and query n + 16's in register 1
+  // (see AttnMfmaRun, x == NDT).
   v4f lacc;
-  float m;       // lazy row max (log2 domain)
-  float ldelta;  // repair: running sum of the exact-minus-code corrections (lane's keys)
+  float m;  // lazy row max (log2 domain)
 
   __device__ __forceinline__ void init() {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        o[dt][i] = 0.0f;
-        if constexpr (DO_REPAIR) orep[dt][i] = 0.0f;
-      }
+      for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) lacc[i] = 0.0f;
     m = kAttnNeg;
-    ldelta = 0.0f;
   }
 
-  // O, O_r, l *= alpha (a moved lazy max)
+  // O, l *= alpha (a moved lazy max)
   __device__ __forceinline__ void rescale(float alpha) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-      if constexpr (DO_REPAIR) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) orep[dt][i] *= alpha;
-      }
-    }
     // register 1 of lane n holds query n + 16's sum: it takes that query's alpha
     const float alpha16 = __shfl(alpha, ((int)(__lane_id() & 15)) + 16, 64);
     lacc[0] *= alpha;
     lacc[1] *= alpha16;
-    if constexpr (DO_REPAIR) ldelta *= alpha;
   }
 };
-
-// e4m3 value of a P code (codes are 0 or in [8, 126], i.e. zero or normal).
-__device__ __forceinline__ float p_value(uint32_t code) {
-  return code ? __uint_as_float((code << 20) + 0x3C000000u) : 0.0f;
-}
 
 // Lane offsets of the 16-byte LDS chunks a lane reads for its MFMA A fragments.  Row
 // 32x + r of a swizzled tile has the same swizzle as row r (lds_swz depends on row / 2 or
@@ -377,11 +370,25 @@ __device__ __forceinline__ v8i lds_pair(const uint8_t* base, int o0, int o1) {
   return r;
 }
 
+// E8M0 block scale of the repair operands: the two e4m3 parts of 8 delta are multiplied
+// by 2^-3 inside the product (127 = 1.0).
+constexpr int kRepairScaleE8M0 = 124;
+
+// B operands of the PV products of one tile: the P codes and, with the repair, the two
+// e4m3 parts hi + lo = 8 delta of the corrections (zero where no correction applies).
+template <bool REP>
+struct AttnPB {
+  v8i p[2];
+  v8i hi[REP ? 2 : 1];
+  v8i lo[REP ? 2 : 1];
+};
+
 // A run of matrix-core products with their A fragments fetched from LDS three products
 // ahead (four fragments in flight), so the products issue back to back instead of each
 // waiting for its own LDS read.  The run is the PV products of one tile (when PV: O^T tile
-// x of key half kh, or the row-sum product when x == D/32) followed by the QK^T products
-// of another (when QK: subtile u, half hh).
+// x of key half kh, or the row-sum product when x == D/32; with REP each fragment also
+// multiplies the two repair parts) followed by the QK^T products of another (when QK:
+// subtile u, half hh).
 template <int D, bool PV, bool QK, int AHEAD = 3>
 struct AttnMfmaRun {
   static constexpr int RING = AHEAD + 1;
@@ -403,14 +410,27 @@ struct AttnMfmaRun {
   }
 
   template <int K, bool REP>
-  __device__ static __forceinline__ void exec(const v8i& fr, const v8i (&pf)[2], const v8i (&qf)[D / 64],
-                                              v16f (&s)[4], AttnState<D, REP>& st) {
+  __device__ static __forceinline__ void exec(const v8i& fr, const AttnPB<REP>& pb, const v8i (&qf)[D / 64],
+                                              v16f (&s)[4], AttnState<D>& st) {
     if constexpr (K < NPV) {
       constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
-      if constexpr (x == NDT)
-        st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pf[kh], st.lacc, 0, 0, 0, 0, 0, 0);
-      else
-        st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pf[kh], st.o[x], 0, 0, 0, 0, 0, 0);
+      if constexpr (x == NDT) {
+        st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pb.p[kh], st.lacc, 0, 0, 0, 0, 0, 0);
+        if constexpr (REP) {
+          st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pb.hi[kh], st.lacc, 0, 0, 0, 127, 0,
+                                                                     kRepairScaleE8M0);
+          st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pb.lo[kh], st.lacc, 0, 0, 0, 127, 0,
+                                                                     kRepairScaleE8M0);
+        }
+      } else {
+        st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pb.p[kh], st.o[x], 0, 0, 0, 0, 0, 0);
+        if constexpr (REP) {
+          st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pb.hi[kh], st.o[x], 0, 0, 0, 127, 0,
+                                                                    kRepairScaleE8M0);
+          st.o[x] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr, pb.lo[kh], st.o[x], 0, 0, 0, 127, 0,
+                                                                    kRepairScaleE8M0);
+        }
+      }
     } else {
       constexpr int u = (K - NPV) / QKM, hh = (K - NPV) % QKM;
       if constexpr (hh == 0) {
@@ -426,15 +446,15 @@ struct AttnMfmaRun {
 
   template <int K, bool REP>
   __device__ static __forceinline__ void seq(v8i (&fr)[RING], const uint8_t* sV, const uint8_t* sK,
-                                             const AttnFragOfs<D>& fo, const v8i (&pf)[2], const v8i (&qf)[D / 64],
-                                             v16f (&s)[4], AttnState<D, REP>& st) {
+                                             const AttnFragOfs<D>& fo, const AttnPB<REP>& pb,
+                                             const v8i (&qf)[D / 64], v16f (&s)[4], AttnState<D>& st) {
     if constexpr (K < N) {
       if constexpr (K + AHEAD < N) fr[(K + AHEAD) % RING] = frag<K + AHEAD>(sV, sK, fo);
-      exec<K, REP>(fr[K % RING], pf, qf, s, st);
+      exec<K, REP>(fr[K % RING], pb, qf, s, st);
       // keep program order: a reordered run would hold the scores and the PV fragments
       // live together
       __builtin_amdgcn_sched_barrier(0);
-      seq<K + 1, REP>(fr, sV, sK, fo, pf, qf, s, st);
+      seq<K + 1, REP>(fr, sV, sK, fo, pb, qf, s, st);
     }
   }
 
@@ -450,11 +470,11 @@ struct AttnMfmaRun {
 
   template <bool REP>
   __device__ static __forceinline__ void run(const uint8_t* sV, const uint8_t* sK, const AttnFragOfs<D>& fo,
-                                             const v8i (&pf)[2], const v8i (&qf)[D / 64], v16f (&s)[4],
-                                             AttnState<D, REP>& st) {
+                                             const AttnPB<REP>& pb, const v8i (&qf)[D / 64], v16f (&s)[4],
+                                             AttnState<D>& st) {
     v8i fr[RING];
     prime<0>(fr, sV, sK, fo);
-    seq<0, REP>(fr, sV, sK, fo, pf, qf, s, st);
+    seq<0, REP>(fr, sV, sK, fo, pb, qf, s, st);
   }
 };
 
@@ -522,7 +542,7 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
 }
 
 // Row max of the tile, the lazy-max decision and the exp2-free P codes.  Returns the new
-// row max m_new of the lane's query; pf receives the codes (the PV B operand).
+// row max m_new of the lane's query; pb.p receives the codes (the PV B operand).
 //
 // code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
 // 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
@@ -535,8 +555,18 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
 // 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
 // FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
 // keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
-template <bool HAS_BIAS>
-__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, v8i (&pf)[2]) {
+//
+// Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
+// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
+// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
+// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
+// hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
+// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
+// significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
+// lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
+template <bool HAS_BIAS, bool REP>
+__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, float tau,
+                                            AttnPB<REP>& pb) {
   // row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic), as four
   // independent v_max3 chains so that the VALU need not wait on each result
   float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -563,12 +593,13 @@ __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float 
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4) {
       uint32_t tb[4];
+      float bits[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x = s[t][4 * w4 + e];
-        const float bits = __builtin_fmaf(x, c8, cst);
+        bits[e] = __builtin_fmaf(x, c8, cst);
         const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, c8f, cstf), 0.0f, 1.0f);
-        tb[e] = __float_as_uint(__builtin_fmaf(bits, keep, 12582912.0f));
+        tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
       }
       // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
       const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
@@ -576,69 +607,37 @@ __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float 
       // An empty use keeps the codes here instead of letting them sink to their consumer
       // (the PV products, which the ping-pong kernel issues in another phase).
       asm volatile("" ::"v"(word));
-      pf[t >> 1][4 * (t & 1) + w4] = (int)word;
+      pb.p[t >> 1][4 * (t & 1) + w4] = (int)word;
+      if constexpr (REP) {
+        const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+        const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
+        const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
+        float d8[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
+          const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
+          const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
+          d8[e] = papx[e] >= tau ? d : 0.0f;
+        }
+        int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
+        const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
+        pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
+        pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
+      }
     }
   }
   return m_new;
 }
 
-// Repair: delta = exp2(S - m) - P where P >= tau; O_r^T += bf16(V^T) bf16(delta^T) over
-// 16-key chunks: chunk (t, u) gives lane group g the 8 keys 64(t/2) + 16(t%2) + 32g + 8u + 0..7.
-template <int D, bool HAS_BIAS>
-__device__ __forceinline__ void attn_repair(const uint8_t* sV, const v16f (&s)[4], const v8i (&pf)[2], float sq,
-                                            float skj, float m_new, float tau, int lane, AttnState<D, true>& st) {
-  constexpr int NDT = D / 32;
-  const int g = lane >> 5;
-  float dsum = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      v8bf db;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 8 * u + e;
-        const uint32_t code = ((uint32_t)pf[t >> 1][4 * (t & 1) + (i >> 2)] >> (8 * (i & 3))) & 0xffu;
-        const float papx = p_value(code);
-        const float S = HAS_BIAS ? s[t][i] : (s[t][i] * sq) * skj;
-        const float pexact = __builtin_amdgcn_exp2f(S - m_new);  // invalid keys: S = -inf -> 0
-        const float d = (papx >= tau) ? (pexact - papx) : 0.0f;
-        dsum += d;
-        db[e] = __builtin_bit_cast(__bf16, (unsigned short)f32_to_bf16_bits(d));
-      }
-      const int key0 = 64 * (t >> 1) + 16 * (t & 1) + 32 * g + 8 * u;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int row = 32 * dt + (lane & 31);
-        const int c = key0 >> 4;
-        const uint8_t* src = sV + row * 128 + ((c ^ lds_swz<128>(row)) << 4) + (key0 & 15);
-        const v2i raw = *reinterpret_cast<const v2i*>(src);
-        v8bf vb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t byte = ((uint32_t)raw[e >> 2] >> (8 * (e & 3))) & 0xffu;
-          // e4m3 -> bf16 is exact: rebias the exponent (7 -> 127) and widen the mantissa.
-          const uint32_t sgn = (byte & 0x80u) << 8, mag = byte & 0x7fu;
-          uint32_t bits;
-          if (mag >= 8u) {
-            bits = sgn | ((mag + (120u << 3)) << 4);
-          } else {  // subnormal: mag * 2^-9
-            const float f = (float)mag * 0.001953125f;
-            bits = sgn | (__float_as_uint(f) >> 16);
-          }
-          vb[e] = __builtin_bit_cast(__bf16, (unsigned short)bits);
-        }
-        st.orep[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, db, st.orep[dt], 0, 0, 0);
-      }
-    }
-  }
-  st.ldelta += dsum;
-}
-
-// O = (O + O_r) * sv / max(l, 1e-12) -> out (bf16 / fp16 through its strides).  The lane
-// holds query qrow, channels 32 dt + 8 (i/4) + 4 g + i%4.
-template <int D, bool DO_REPAIR, int ODT>
-__device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, const float* sv, int bh, int b, int h,
+// O = (O + O_r) * sv / max(l, 1e-12) -> out (bf16 / fp16 through its strides; O_r is inside
+// O).  The lane holds query qrow, channels 32 dt + 8 (i/4) + 4 g + i%4.
+template <int D, int ODT>
+__device__ __forceinline__ void attn_store(const AttnState<D>& st, const float* sv, int bh, int b, int h,
                                            int qrow, int lane, void* out, int64_t os_b, int64_t os_h, int64_t os_s,
                                            int64_t os_d) {
   constexpr int NDT = D / 32;
@@ -646,8 +645,7 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
   // row sum of this lane's query q = lane % 32: register q / 16 of lane q % 16
   const int q = lane & 31;
   const float l0 = __shfl(st.lacc[0], q & 15, 64), l1 = __shfl(st.lacc[1], q & 15, 64);
-  float l = q < 16 ? l0 : l1;
-  if constexpr (DO_REPAIR) l += st.ldelta + __shfl_xor(st.ldelta, 32, 64);
+  const float l = q < 16 ? l0 : l1;
   const float den = fmaxf(l, 1.0e-12f);
   // (acc * sv) / den correctly rounded from one reciprocal per row (div_by_scale: the
   // quotients are O's values and den lies in [1e-12, ~1e7], so nothing over- or underflows)
@@ -663,9 +661,7 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
       uint32_t ob[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float acc = st.o[dt][4 * q4 + e];
-        if constexpr (DO_REPAIR) acc += st.orep[dt][4 * q4 + e];
-        const float v = div_by_scale(acc * sv4[e], den, rden);
+        const float v = div_by_scale(st.o[dt][4 * q4 + e] * sv4[e], den, rden);
         ob[e] = ODT == MXF8_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
       }
       uint16_t* dst = reinterpret_cast<uint16_t*>(obase) + (int64_t)d0 * os_d;
@@ -680,18 +676,14 @@ __device__ __forceinline__ void attn_store(const AttnState<D, DO_REPAIR>& st, co
 }
 
 // ---------------------------------------------------------------------------------------
-// One tile at a time: per KV tile, S = QK^T, codes, PV (and the repair).  Without repair
-// two waves per SIMD fit (256 VGPRs); the repair keeps more live and runs one.
+// One tile at a time: per KV tile, S = QK^T, codes (and the repair parts), PV.  Two waves
+// per SIMD (256 registers each), so one wave's softmax overlaps the other's products.
 // ---------------------------------------------------------------------------------------
-template <bool DO_REPAIR>
-struct AttnOccupancy {
-  static constexpr int waves = DO_REPAIR ? 1 : 2;
-};
 
 // QF: Q arrives as 16-bit values of the output's dtype (qa) and each workgroup quantizes
 // its own 128-row block while its first KV tile is in flight; q8 / sq are then unused.
 template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT, bool QF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOccupancy<DO_REPAIR>::waves)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
                      const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
                      const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
@@ -705,7 +697,7 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
   const int nk = cx.nk, lane = cx.lane;
   const AttnFragOfs<D> fo(lane);
 
-  AttnState<D, DO_REPAIR> st;
+  AttnState<D> st;
   st.init();
 
   const int j0 = (int)(((int64_t)cx.I * nk) / nq);
@@ -732,19 +724,18 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     const float skj = cx.skh[j];
     const int kv0 = j * 128;
     v16f s[4];
-    v8i pf[2];
-    AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+    AttnPB<DO_REPAIR> pb;
+    AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-    const float m_new = attn_codes<HAS_BIAS>(s, cx.sqI, skj, st.m, pf);
+    const float m_new = attn_codes<HAS_BIAS, DO_REPAIR>(s, cx.sqI, skj, st.m, tau, pb);
     if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
     st.m = m_new;
-    AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
-    if constexpr (DO_REPAIR) attn_repair<D, HAS_BIAS>(buf + T::KB, s, pf, cx.sqI, skj, m_new, tau, lane, st);
+    AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
   }
   if (cx.qrow >= Sq) return;
-  attn_store<D, DO_REPAIR, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+  attn_store<D, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -836,7 +827,7 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     for (int hh = 0; hh < D / 64; ++hh) cx.qf[hh] = qnext[hh];
     cx.sqI = sqnext;
     const int np = p + 2 < seg_end ? p + 2 : seg_end;  // first tile of the next pair
-    AttnState<D, false> st;
+    AttnState<D> st;
     if (active) {
       st.init();
       int j = (int)(((int64_t)cx.I * nk) / nq);
@@ -845,14 +836,14 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         const float skj = cx.skh[j];
         const int kv0 = j * 128;
         v16f s[4];
-        v8i pf[2];
-        AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+        AttnPB<false> pb;
+        AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-        const float m_new = attn_codes<HAS_BIAS>(s, cx.sqI, skj, st.m, pf);
+        const float m_new = attn_codes<HAS_BIAS, false>(s, cx.sqI, skj, st.m, -1.0f, pb);
         if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
         st.m = m_new;
-        AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pf, cx.qf, s, st);
+        AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         j = j + 1 == nk ? 0 : j + 1;
       }
     }
@@ -861,7 +852,7 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       fetch_q(pair_item(np, nact));
     }
     if (active && cx.qrow < Sq)
-      attn_store<D, false, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+      attn_store<D, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
     p = np;
   }
 }

@@ -63,7 +63,6 @@ __device__ __forceinline__ float gelu_tanh_f32(float z) {
 }
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef float v2f __attribute__((ext_vector_type(2)));
 
 // fp32 -> bf16 -> fp32 and fp32 pair -> packed bf16 pair, both with the hardware
 // round-to-nearest-even conversion (v_cvt_pk_bf16_f32).

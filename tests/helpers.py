@@ -50,3 +50,17 @@ def assert_attn_close(out, ref, cos_min=0.999, max_abs=2e-2):
     c = cos(out, ref)
     m = float(np.max(np.abs(np.asarray(out, np.float64) - np.asarray(ref, np.float64))))
     assert c >= cos_min and m <= max_abs, (c, m)
+
+
+def assert_ln_close(y, ref, what):
+    """LayerNorm output bar: equal almost everywhere; elsewhere within 1 bf16 ulp, or within
+    2^-17 absolute where n (1 + scale) and shift cancel (the result's ulp is then far below
+    the operands' fp32 rounding)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    mag = np.maximum(np.abs(y), np.abs(ref))
+    ulp = np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 7), 2.0 ** -133)
+    err = np.abs(y - ref)
+    bad = (err > ulp) & (err > 2.0 ** -17)
+    assert not bad.any(), (what, err[bad][:5], y[bad][:5], ref[bad][:5])
+    assert (err > 0).mean() < 5e-3, (what, (err > 0).mean())

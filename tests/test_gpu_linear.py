@@ -8,7 +8,7 @@ import torch.nn.functional as F
 
 from oracle import linear as ol
 from oracle.numerics import bf16_round, e4m3_decode
-from tests.helpers import assert_gemm_close, bf16_randn, codes, to_gpu, with_outliers
+from tests.helpers import assert_gemm_close, assert_ln_close, bf16_randn, codes, to_gpu, with_outliers
 
 pytestmark = pytest.mark.gpu
 
@@ -387,20 +387,6 @@ def test_720p_linear_lora_sampled_rows(fl, N, K, gelu):
 
 # ---------------------------------------------------------------- adaLN modulation + quantization
 
-def _assert_ln_close(y, ref, what):
-    """LayerNorm output bar: equal almost everywhere; elsewhere within 1 bf16 ulp, or within
-    2^-17 absolute where n (1 + scale) and shift cancel (the result's ulp is then far below
-    the operands' fp32 rounding)."""
-    y = np.asarray(y, np.float64)
-    ref = np.asarray(ref, np.float64)
-    mag = np.maximum(np.abs(y), np.abs(ref))
-    ulp = np.where(mag > 0, 2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 7), 2.0 ** -133)
-    err = np.abs(y - ref)
-    bad = (err > ulp) & (err > 2.0 ** -17)
-    assert not bad.any(), (what, err[bad][:5], y[bad][:5], ref[bad][:5])
-    assert (err > 0).mean() < 5e-3, (what, (err > 0).mean())
-
-
 def _eager_modulate(nb, shift_rows, scale_rows):
     """torch's eager bf16 ops after the LayerNorm output nb (bf16 values)."""
     op = bf16_round((1.0 + scale_rows.astype(np.float64)).astype(np.float32)).astype(np.float64)
@@ -469,7 +455,7 @@ def test_adaln_quant_general_rows(fl, B, S, C):
             rows = np.arange(B * S) // S
             _assert_eager_from_ln_neighbours(yk, bf16_round(n.astype(np.float32)), shift[rows], scale[rows], eager)
         else:
-            _assert_ln_close(yk, ol.adaln_modulate(x.reshape(-1, C), shift, scale, S), eager)
+            assert_ln_close(yk, ol.adaln_modulate(x.reshape(-1, C), shift, scale, S), eager)
         rc, rs = ol.quantize_rows(yk)
         np.testing.assert_array_equal(codes(x8), rc)
         np.testing.assert_array_equal(sa.cpu().numpy(), rs)
@@ -505,7 +491,7 @@ def test_adaln_quant_matches_torch_gpu_ops(fl):
             np.testing.assert_array_equal(_eager_modulate(nb_torch, sh, sc), ref.float().reshape(B * S, C).cpu().numpy())
             _assert_eager_from_ln_neighbours(yk, nb_torch, sh, sc, eager)
         else:
-            _assert_ln_close(yk, ref.float().reshape(B * S, C).cpu().numpy(), eager)
+            assert_ln_close(yk, ref.float().reshape(B * S, C).cpu().numpy(), eager)
 
 
 @pytest.mark.parametrize("lora", [False, True])

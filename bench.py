@@ -200,11 +200,8 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bo
     for name, q, k, v, mask in attn_inputs:
         sfx = "" if name == "attn" else f"[{name}]"
         c = ops.softmax_c(None, HEAD_DIM)
-        t = tick("attn_kmean+quant_k" + sfx)
-        k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
-        tock(t)
-        t = tick("attn_quant_v" + sfx)
-        v8t, sv = ops.attn_quant_v(v)
+        t = tick("attn_quant_kv" + sfx)
+        k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
         tock(t)
         if fuse_q:
             # the Q quantizer runs inside the attention launch
@@ -410,16 +407,17 @@ def main() -> int:
         parts["attn_fwd" + sfx] = flop_part(f, t)
         if biggest is None or f > biggest[1]:
             biggest = ("attn_fwd" + sfx, f, t)
+        # K and V: one pass over both credited (3 bytes per element) plus their scales
         for qname, nelem, nscale in (("attn_quant_q", b * HEADS * sq * HEAD_DIM, b * HEADS * math.ceil(sq / 128)),
-                                     ("attn_kmean+quant_k", b * HEADS * sk * HEAD_DIM, b * HEADS * math.ceil(sk / 128)),
-                                     ("attn_quant_v", b * HEADS * sk * HEAD_DIM, b * HEADS * HEAD_DIM)):
+                                     ("attn_quant_kv", 2 * b * HEADS * sk * HEAD_DIM,
+                                      b * HEADS * (math.ceil(sk / 128) + HEAD_DIM))):
             if qname + sfx in kern:  # attn_quant_q only when Q is quantized in its own launch
                 parts[qname + sfx] = byte_part(3 * nelem + 4 * nscale, kern[qname + sfx])
     # end-to-end wrappers over the same FLOPs: FP8Linear.forward (activation quantizer or
     # fused adaLN quantizer, LoRA down-projection, GEMM) and fp8_attention (quantizers +
     # attention), from the per-part event times
     lin_ms = sum(v for k, v in kern.items() if k.split("[")[0] in ("quant_rows", "adaln_quant", "lora_down", "gemm"))
-    att_ms = attn_ms + sum(v for k, v in kern.items() if k.startswith(("attn_quant", "attn_kmean")))
+    att_ms = attn_ms + sum(v for k, v in kern.items() if k.startswith("attn_quant"))
     step_flops = gemm_f + attn_f
     value = step_flops / (ms_step * 1e-3) / 1e12
     _, af, t_attn = biggest

@@ -146,6 +146,25 @@ int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides[4],
                       int64_t B, int64_t H, int64_t S, int64_t D,
                       uint8_t* v8t, float* sv, void* workspace, hipStream_t stream);
 
+/* Scratch bytes needed by mxf8_attn_quant_kv. */
+int64_t mxf8_attn_kv_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D);
+
+/*
+ * K and V quantizers together.  Replaces k.float().mean(dim=2) (kernels/fp8_attention.py:338),
+ * _quantize_k_kernel (80-119, launch 339-354) and _quantize_v_kernel (122-170, launch
+ * 356-369) of one attention call: the same outputs as mxf8_attn_kmean + mxf8_attn_quant_k +
+ * mxf8_attn_quant_v, in three launches (one pass over K and V for the key mean and the
+ * per-channel V amax, one fold of both, one pass that quantizes K and V).
+ *   k, v [B, H, S, D] of `dtype` with element strides k_strides[4], v_strides[4]
+ *   k8 [B, H, Skp, D], sk [B, H, ceil(S/128)], v8t [B, H, D, Skp], sv [B, H, D] (written)
+ *   mean [B, H, D] fp32 key mean (written when not NULL; kept in `workspace` otherwise)
+ *   workspace: mxf8_attn_kv_workspace_bytes(B, H, S, D) bytes.  Deterministic.
+ */
+int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                       int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                       uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean, void* workspace,
+                       hipStream_t stream);
+
 /*
  * FP8 flash-attention forward.  Replaces _fp8_attn_kernel (kernels/fp8_attention.py:185-297,
  * launch 380-402) with BLOCK_N = 128: log2-domain scores, staggered KV visit order, lazy

@@ -326,20 +326,17 @@ __device__ __forceinline__ void load8(const void* base, const Strides4& st, int6
   }
 }
 
-// Q (IS_K = false) and K (IS_K = true) quantizer: one block per (128-row block, b*H + h).
-// Thread t handles the 8-wide d-chunk (t % CPR) of rows (t / CPR) + RPP * p.
+// Q (IS_K = false) and K (IS_K = true) quantizer of one (128-row block blk, b*H + h) tile
+// by a 256-thread block (nblk blocks per head; red: 4 floats of LDS).  Thread t handles
+// the 8-wide d-chunk (t % CPR) of rows (t / CPR) + RPP * p.
 template <int DT, int D, bool IS_K, bool VEC>
-__global__ __launch_bounds__(256) void attn_quant_qk_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
-                                                            int64_t S, int64_t Sp, float c,
-                                                            const float* __restrict__ mean,
-                                                            uint8_t* __restrict__ out8,
-                                                            float* __restrict__ scale_out) {
+__device__ __forceinline__ void quant_qk_tile(const void* __restrict__ src, const Strides4& st, int64_t H, int64_t S,
+                                              int64_t Sp, float c, const float* __restrict__ mean,
+                                              uint8_t* __restrict__ out8, float* __restrict__ scale_out, int64_t blk,
+                                              int64_t bh, int64_t nblk, float* red) {
   constexpr int CPR = D / 8;      // chunks per row
   constexpr int RPP = 256 / CPR;  // rows per pass
   constexpr int NP = 128 / RPP;   // passes
-  __shared__ float red[4];
-  const int64_t blk = blockIdx.x;
-  const int64_t bh = blockIdx.y;
   const int64_t b = bh / H, h = bh % H;
   const void* base = static_cast<const char*>(src) + (b * st.b + h * st.h) * (int64_t)sizeof(typename Elem<DT>::T);
   const int cc = threadIdx.x % CPR;
@@ -392,7 +389,19 @@ __global__ __launch_bounds__(256) void attn_quant_qk_kernel(const void* __restri
     o.y = cvt4_e4m3(q[4], q[5], q[6], q[7]);
     *reinterpret_cast<uint2*>(out8 + (bh * Sp + s) * D + cc * 8) = o;
   }
-  if (threadIdx.x == 0) scale_out[bh * gridDim.x + blk] = sc;
+  if (threadIdx.x == 0) scale_out[bh * nblk + blk] = sc;
+}
+
+// One block per (128-row block, b*H + h).
+template <int DT, int D, bool IS_K, bool VEC>
+__global__ __launch_bounds__(256) void attn_quant_qk_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
+                                                            int64_t S, int64_t Sp, float c,
+                                                            const float* __restrict__ mean,
+                                                            uint8_t* __restrict__ out8,
+                                                            float* __restrict__ scale_out) {
+  __shared__ float red[4];
+  quant_qk_tile<DT, D, IS_K, VEC>(src, st, H, S, Sp, c, mean, out8, scale_out, blockIdx.x, blockIdx.y, gridDim.x,
+                                  red);
 }
 
 // Partial column reductions over a chunk of rows: SUM (key mean) or ABSMAX (V scale).
@@ -448,17 +457,13 @@ __global__ __launch_bounds__(256) void attn_colreduce_kernel(const void* __restr
   }
 }
 
-// Fold of the per-chunk slabs part[bh][chunk][d]: SUM -> out = sum / S (the key mean),
-// ABSMAX -> out = max(amax, 1e-12) / 448 (the per-channel V scale).  One block per (b, h):
-// 256 / D threads per channel each fold a contiguous quarter / half of the chunks with
-// eight independent partial results (loads in flight together), then the parts are
-// combined in a fixed order, so the result does not depend on scheduling.
+// Fixed-order fold of one statistic's slabs part[bh][chunk][d] by 256 threads (PARTS =
+// 256 / D threads per channel, each folding a contiguous part of the chunks with eight
+// independent partial results, then combined in a fixed order).  Returns the channel's
+// total to the threads with threadIdx.x < D (d = threadIdx.x).  red: [256] floats of LDS.
 template <int D, bool ABSMAX>
-__global__ __launch_bounds__(256) void attn_colfold_kernel(const float* __restrict__ part, int nch, int64_t S,
-                                                           float* __restrict__ out) {
+__device__ __forceinline__ float colfold(const float* __restrict__ part, int nch, int64_t bh, float* red) {
   constexpr int PARTS = 256 / D;
-  __shared__ float red[PARTS][D];
-  const int64_t bh = blockIdx.x;
   const int d = threadIdx.x % D, p = threadIdx.x / D;
   const int c0 = p * nch / PARTS, c1 = (p + 1) * nch / PARTS;
   const float* src = part + (bh * nch) * D + d;
@@ -481,33 +486,52 @@ __global__ __launch_bounds__(256) void attn_colfold_kernel(const float* __restri
   for (int w = 4; w >= 1; w >>= 1)
 #pragma unroll
     for (int i = 0; i < w; ++i) acc[i] = ABSMAX ? fmaxf(acc[i], acc[i + w]) : acc[i] + acc[i + w];
-  red[p][d] = acc[0];
+  red[p * D + d] = acc[0];
   __syncthreads();
+  float a = 0.0f;
   if (p == 0) {
-    float a = red[0][d];
+    a = red[d];
 #pragma unroll
-    for (int j = 1; j < PARTS; ++j) a = ABSMAX ? fmaxf(a, red[j][d]) : a + red[j][d];
-    out[bh * D + d] = ABSMAX ? e4m3_scale(a) : __fdiv_rn(a, (float)S);
+    for (int j = 1; j < PARTS; ++j) a = ABSMAX ? fmaxf(a, red[j * D + d]) : a + red[j * D + d];
   }
+  __syncthreads();
+  return a;
 }
 
-// V quantizer, transposed store.  grid (Skp/128, B*H).  Each block quantizes a 128-key x
-// D tile with the per-channel scales sv (from attn_colfold_kernel) and writes it transposed
-// through LDS so that every v8t row segment is a full 128 bytes.
-// Thread t handles d-chunk (t % CPR) of the 4 consecutive keys 4 * (t / CPR + KQP * p) + 0..3.
+// Fold of the per-chunk slabs of one statistic (grid B*H): SUM -> out = sum / S (the key
+// mean), ABSMAX -> out = max(amax, 1e-12) / 448 (the per-channel V scale).
+template <int D, bool ABSMAX>
+__global__ __launch_bounds__(256) void attn_colfold_kernel(const float* __restrict__ part, int nch, int64_t S,
+                                                           float* __restrict__ out) {
+  __shared__ float red[256];
+  const int64_t bh = blockIdx.x;
+  const float a = colfold<D, ABSMAX>(part, nch, bh, red);
+  if (threadIdx.x < D) out[bh * D + threadIdx.x] = ABSMAX ? e4m3_scale(a) : __fdiv_rn(a, (float)S);
+}
+
+// V quantizer of one (128-key tile blk, b*H + h), transposed store: the block quantizes a
+// 128-key x D tile with the per-channel scales sv and writes it transposed through LDS so
+// that every v8t row segment is a full 128 bytes.  Thread t handles d-chunk (t % CPR) of
+// the 4 consecutive keys 4 * (t / CPR + KQP * p) + 0..3.
+template <int D>
+struct QuantVLds {
+  static constexpr int STRIDE = 128 + 4;  // LDS row stride of the transposed tile
+  uint8_t tile[D * STRIDE];
+  float s_sv[D];
+  float s_r[D];
+};
+
 template <int DT, int D, bool VEC>
-__global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
-                                                           int64_t S, int64_t Sp, const float* __restrict__ sv,
-                                                           uint8_t* __restrict__ v8t) {
+__device__ __forceinline__ void quant_v_tile(const void* __restrict__ src, const Strides4& st, int64_t H, int64_t S,
+                                             int64_t Sp, const float* __restrict__ sv, uint8_t* __restrict__ v8t,
+                                             int64_t blk, int64_t bh, QuantVLds<D>& L) {
   constexpr int CPR = D / 8;
   constexpr int KQP = 256 / CPR;  // key quads per pass
   constexpr int NP = 32 / KQP;    // passes over the 32 key quads of the tile
-  constexpr int LDS_STRIDE = 128 + 4;
-  __shared__ uint8_t tile[D * LDS_STRIDE];
-  __shared__ float s_sv[D];
-  __shared__ float s_r[D];
-  const int64_t blk = blockIdx.x;
-  const int64_t bh = blockIdx.y;
+  constexpr int LDS_STRIDE = QuantVLds<D>::STRIDE;
+  uint8_t* const tile = L.tile;
+  float* const s_sv = L.s_sv;
+  float* const s_r = L.s_r;
   const int64_t b = bh / H, h = bh % H;
   if (threadIdx.x < D) {
     const float s = sv[bh * D + threadIdx.x];
@@ -568,6 +592,126 @@ __global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restric
     uint4 o = make_uint4(src4[0], src4[1], src4[2], src4[3]);
     *reinterpret_cast<uint4*>(v8t + (bh * D + d) * Sp + blk * 128 + kc * 16) = o;
   }
+}
+
+// One block per (128-key tile, b*H + h).
+template <int DT, int D, bool VEC>
+__global__ __launch_bounds__(256) void attn_quant_v_kernel(const void* __restrict__ src, Strides4 st, int64_t H,
+                                                           int64_t S, int64_t Sp, const float* __restrict__ sv,
+                                                           uint8_t* __restrict__ v8t) {
+  __shared__ QuantVLds<D> L;
+  quant_v_tile<DT, D, VEC>(src, st, H, S, Sp, sv, v8t, blockIdx.x, blockIdx.y, L);
+}
+
+// ---------------------------------------------------------------------------------------
+// K and V of one attention together (kernels/fp8_attention.py:338-369): one pass over both
+// for the statistics that need the whole sequence (the key mean, the per-channel V amax),
+// one fold of both, then one launch that quantizes a 128-key tile of K and of V per block.
+// The second read of K and V follows the first closely, so it is mostly served by the
+// MALL; in the fused QKV layout ([B, S, 2, H, D]) the two reads of a key's K and V rows
+// are adjacent.
+// ---------------------------------------------------------------------------------------
+
+// Partial column statistics over a chunk of keys: part[0][bh][chunk][d] = sum of k,
+// part[1][bh][chunk][d] = max |v| (grid (B*H, nch): heads fastest, so the blocks that run
+// together read the same keys' rows, which in a [B, S, (2,) H, D] layout are adjacent).
+template <int DT, int D, bool VECK, bool VECV>
+__global__ __launch_bounds__(256) void attn_kv_colreduce_kernel(const void* __restrict__ k, Strides4 stk,
+                                                                const void* __restrict__ v, Strides4 stv, int64_t H,
+                                                                int64_t S, int64_t rows_per_chunk,
+                                                                float* __restrict__ part) {
+  constexpr int CPR = D / 8;
+  constexpr int RPP = 256 / CPR;
+  __shared__ float red[2][RPP][D + 1];
+  const int64_t ch = blockIdx.y, nch = gridDim.y;
+  const int64_t bh = blockIdx.x, BH = gridDim.x;
+  const int64_t b = bh / H, h = bh % H;
+  constexpr int64_t ES = sizeof(typename Elem<DT>::T);
+  const void* kb = static_cast<const char*>(k) + (b * stk.b + h * stk.h) * ES;
+  const void* vb = static_cast<const char*>(v) + (b * stv.b + h * stv.h) * ES;
+  const int cc = threadIdx.x % CPR;
+  const int rl = threadIdx.x / CPR;
+  const int64_t r0 = ch * rows_per_chunk;
+  const int64_t r1 = min(S, r0 + rows_per_chunk);
+  float ks[8], va[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ks[i] = va[i] = 0.0f;
+  int64_t s = r0 + rl;
+  if constexpr (VECK && VECV) {
+    // 4 rows of K and of V in flight together; rows are folded in the same order as one
+    // at a time
+    constexpr int U = 4;
+    for (; s + (U - 1) * RPP < r1; s += U * RPP) {
+      uint4 rk[U], rv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        rk[u] = raw8<DT>(kb, stk, s + u * RPP, cc * 8);
+        rv[u] = raw8<DT>(vb, stv, s + u * RPP, cc * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float fk[8], fv[8];
+        cvt8<DT>(rk[u], fk);
+        cvt8<DT>(rv[u], fv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ks[i] += fk[i];
+          va[i] = fmaxf(va[i], fabsf(fv[i]));
+        }
+      }
+    }
+  }
+  for (; s < r1; s += RPP) {
+    float fk[8], fv[8];
+    load8<DT, VECK>(kb, stk, s, cc * 8, fk);
+    load8<DT, VECV>(vb, stv, s, cc * 8, fv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ks[i] += fk[i];
+      va[i] = fmaxf(va[i], fabsf(fv[i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    red[0][rl][cc * 8 + i] = ks[i];
+    red[1][rl][cc * 8 + i] = va[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * D) {
+    const int t = threadIdx.x / D, d = threadIdx.x % D;
+    float a = red[t][0][d];
+    for (int j = 1; j < RPP; ++j) a = t ? fmaxf(a, red[t][j][d]) : a + red[t][j][d];
+    part[((t * BH + bh) * nch + ch) * D + d] = a;
+  }
+}
+
+// Both folds (grid B*H): mean[bh][d] = sum / S, sv[bh][d] = max(amax, 1e-12) / 448.
+template <int D>
+__global__ __launch_bounds__(256) void attn_kv_fold_kernel(const float* __restrict__ part, int nch, int64_t S,
+                                                           float* __restrict__ mean, float* __restrict__ sv) {
+  __shared__ float red[256];
+  const int64_t bh = blockIdx.x, BH = gridDim.x;
+  const float sum = colfold<D, false>(part, nch, bh, red);
+  const float amax = colfold<D, true>(part + BH * nch * D, nch, bh, red);
+  if (threadIdx.x < D) {
+    mean[bh * D + threadIdx.x] = __fdiv_rn(sum, (float)S);
+    sv[bh * D + threadIdx.x] = e4m3_scale(amax);
+  }
+}
+
+// K tile and V tile of the same 128 keys (grid (B*H, Skp/128)).
+template <int DT, int D, bool VECK, bool VECV>
+__global__ __launch_bounds__(256) void attn_quant_kv_kernel(const void* __restrict__ k, Strides4 stk,
+                                                            const void* __restrict__ v, Strides4 stv, int64_t H,
+                                                            int64_t S, int64_t Sp, const float* __restrict__ mean,
+                                                            const float* __restrict__ sv, uint8_t* __restrict__ k8,
+                                                            float* __restrict__ sk, uint8_t* __restrict__ v8t) {
+  __shared__ float red[4];
+  __shared__ QuantVLds<D> L;
+  // heads fastest: blocks that run together read the same keys' rows
+  const int64_t bh = blockIdx.x, blk = blockIdx.y, nb = gridDim.y;
+  quant_qk_tile<DT, D, true, VECK>(k, stk, H, S, Sp, 0.0f, mean, k8, sk, blk, bh, nb, red);
+  quant_v_tile<DT, D, VECV>(v, stv, H, S, Sp, sv, v8t, blk, bh, L);
 }
 
 static bool attn_vec_ok(const void* p, int dtype, const Strides4& st) {
@@ -776,4 +920,82 @@ extern "C" int mxf8_attn_quant_v(const void* v, int dtype, const int64_t strides
     else launch_quant_v<MXF8_F16, 64>(v, st, vec, H, S, BH, sv, v8t, stream);
   }
   return check_launch("attn_quant_v");
+}
+
+extern "C" int64_t mxf8_attn_kv_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D) {
+  if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return 0;
+  const int64_t BH = B * H;
+  // partial slabs of both statistics, then the key mean
+  return (2 * (int64_t)colreduce_chunks(BH, S) + 1) * BH * D * (int64_t)sizeof(float);
+}
+
+template <int DT, int D>
+static void launch_kv(const void* k, const Strides4& stk, bool veck, const void* v, const Strides4& stv, bool vecv,
+                      int64_t H, int64_t S, int64_t BH, int nch, float* part, float* mean, float* sv, uint8_t* k8,
+                      float* sk, uint8_t* v8t, hipStream_t stream) {
+  const int64_t rpc = cdiv(S, nch);
+  const dim3 rgrid((unsigned)BH, (unsigned)nch);
+  const int64_t nb = cdiv(S, 128);
+  const dim3 qgrid((unsigned)BH, (unsigned)nb);
+#define MXF8_KV_CASE(VK, VV)                                                                                     \
+  if (veck == VK && vecv == VV) {                                                                                \
+    attn_kv_colreduce_kernel<DT, D, VK, VV><<<rgrid, 256, 0, stream>>>(k, stk, v, stv, H, S, rpc, part);         \
+    attn_kv_fold_kernel<D><<<dim3((unsigned)BH), 256, 0, stream>>>(part, nch, S, mean, sv);                       \
+    attn_quant_kv_kernel<DT, D, VK, VV><<<qgrid, 256, 0, stream>>>(k, stk, v, stv, H, S, nb * 128, mean, sv, k8, \
+                                                                    sk, v8t);                                    \
+    return;                                                                                                      \
+  }
+  MXF8_KV_CASE(true, true)
+  MXF8_KV_CASE(true, false)
+  MXF8_KV_CASE(false, true)
+  MXF8_KV_CASE(false, false)
+#undef MXF8_KV_CASE
+}
+
+// K and V quantized together: the key mean, the K quantizer, the per-channel V scale and
+// the transposed V quantizer (kernels/fp8_attention.py:338-369) in three launches.
+static int attn_quant_kv_impl(const char* what, const void* k, const int64_t k_strides[4], const void* v,
+                              const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                              uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean, float* part, int nch,
+                              hipStream_t stream) {
+  const Strides4 stk{k_strides[0], k_strides[1], k_strides[2], k_strides[3]};
+  const Strides4 stv{v_strides[0], v_strides[1], v_strides[2], v_strides[3]};
+  const bool veck = attn_vec_ok(k, dtype, stk), vecv = attn_vec_ok(v, dtype, stv);
+  const int64_t BH = B * H;
+  if (dtype == MXF8_BF16) {
+    if (D == 128) launch_kv<MXF8_BF16, 128>(k, stk, veck, v, stv, vecv, H, S, BH, nch, part, mean, sv, k8, sk, v8t, stream);
+    else launch_kv<MXF8_BF16, 64>(k, stk, veck, v, stv, vecv, H, S, BH, nch, part, mean, sv, k8, sk, v8t, stream);
+  } else {
+    if (D == 128) launch_kv<MXF8_F16, 128>(k, stk, veck, v, stv, vecv, H, S, BH, nch, part, mean, sv, k8, sk, v8t, stream);
+    else launch_kv<MXF8_F16, 64>(k, stk, veck, v, stv, vecv, H, S, BH, nch, part, mean, sv, k8, sk, v8t, stream);
+  }
+  return check_launch(what);
+}
+
+static int attn_quant_kv_checks(const char* what, const void* k, const int64_t k_strides[4], const void* v,
+                                const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                const uint8_t* k8, const float* sk, const uint8_t* v8t, const float* sv) {
+  int rc = attn_common_checks(what, k, dtype, B, H, S, D);
+  if (rc) return rc;
+  if (!v || !k_strides || !v_strides || !k8 || !sk || !v8t || !sv)
+    return set_error(MXF8_EINVAL, "%s: null pointer", what);
+  // the quantizer's grid has one y index per 128-key tile
+  if (cdiv(S, 128) > 65535) return set_error(MXF8_EINVAL, "%s: S must be <= %d", what, 65535 * 128);
+  return MXF8_OK;
+}
+
+extern "C" int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], const void* v,
+                                  const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                  uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean, void* workspace,
+                                  hipStream_t stream) {
+  const char* what = "attn_quant_kv";
+  int rc = attn_quant_kv_checks(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv);
+  if (rc) return rc;
+  if (!workspace) return set_error(MXF8_EINVAL, "%s: null workspace", what);
+  const int64_t BH = B * H;
+  const int nch = colreduce_chunks(BH, S);
+  float* part = static_cast<float*>(workspace);
+  float* mean_ws = part + 2 * (int64_t)nch * BH * D;
+  return attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
+                            mean ? mean : mean_ws, part, nch, stream);
 }

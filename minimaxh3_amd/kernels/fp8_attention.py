@@ -80,9 +80,7 @@ def fp8_attention(
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     c = ops.softmax_c(scale, D)
-    mean = ops.attn_kmean(k)
-    k8, sk = ops.attn_quant_k(k, mean)
-    v8t, sv = ops.attn_quant_v(v)
+    k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
     if fuse_q_quant and ops.attn_fwd_q_supported(q):
         # the attention kernel quantizes Q itself (same codes and scales as attn_quant_q)
         return ops.attn_fwd_q(q, c, k8, v8t, sk, sv, key_mask, key_bias, float(repair_tau), Sk)

@@ -239,6 +239,42 @@ def _(v):
     return v.new_empty((B, H, D, nk * 128), dtype=E4M3), v.new_empty((B, H, D), dtype=torch.float32)
 
 
+@torch.library.custom_op("mxf8::attn_quant_kv", mutates_args=())
+def attn_quant_kv(k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                                            torch.Tensor]:
+    """K and V quantized together (fp8_attention.py:338-369): (K8 [B,H,Skp,D], sk [B,H,nk],
+    V8T [B,H,D,Skp], sv [B,H,D], key mean [B,H,D] fp32) -- the outputs of attn_kmean +
+    attn_quant_k + attn_quant_v in three launches."""
+    _prep(k, "attn_quant_kv")
+    if k.shape != v.shape or k.dtype != v.dtype or k.device != v.device:
+        raise ValueError("attn_quant_kv: k and v must have one shape, dtype and device")
+    B, H, S, D = k.shape
+    nk = _cdiv(S, 128)
+    k8 = torch.empty((B, H, nk * 128, D), dtype=E4M3, device=k.device)
+    sk = torch.empty((B, H, nk), dtype=torch.float32, device=k.device)
+    v8t = torch.empty((B, H, D, nk * 128), dtype=E4M3, device=k.device)
+    sv = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
+    mean = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
+    ws = torch.empty(max(int(N.load().mxf8_attn_kv_workspace_bytes(B, H, S, D)), 16), dtype=torch.uint8,
+                     device=k.device)
+    with torch.cuda.device(k.device):
+        N.check(N.load().mxf8_attn_quant_kv(
+            k.data_ptr(), N.strides4(k), v.data_ptr(), N.strides4(v), N.dtype_code(k.dtype), B, H, S, D,
+            k8.data_ptr(), sk.data_ptr(), v8t.data_ptr(), sv.data_ptr(), mean.data_ptr(), ws.data_ptr(),
+            N.stream_of(k)), "attn_quant_kv")
+    return k8, sk, v8t, sv, mean
+
+
+@attn_quant_kv.register_fake
+def _(k, v):
+    B, H, S, D = k.shape
+    nk = _cdiv(S, 128)
+    f32 = torch.float32
+    return (k.new_empty((B, H, nk * 128, D), dtype=E4M3), k.new_empty((B, H, nk), dtype=f32),
+            k.new_empty((B, H, D, nk * 128), dtype=E4M3), k.new_empty((B, H, D), dtype=f32),
+            k.new_empty((B, H, D), dtype=f32))
+
+
 @torch.library.custom_op("mxf8::attn_fwd", mutates_args=())
 def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Tensor, sk: torch.Tensor,
              sv: torch.Tensor, key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, repair_tau: float,

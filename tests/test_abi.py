@@ -106,3 +106,15 @@ def test_attention_argument_checks(lib):
                                None) == 1 and "D must be" in _err(lib)
     assert lib.mxf8_attn_workspace_bytes(1, 24, 20280, 20280, 128) > 0
     assert lib.mxf8_attn_workspace_bytes(0, 24, 20280, 20280, 128) == 0
+    # K and V together: shape, dtype and pointer checks run before any launch
+    assert lib.mxf8_attn_quant_kv(d, st, d, st, 0, 1, 1, 16, 96, d, d, d, d, None, d, None) == 1 \
+        and "D must be" in _err(lib)
+    assert lib.mxf8_attn_quant_kv(d, st, d, st, 2, 1, 1, 16, 128, d, d, d, d, None, d, None) == 1 \
+        and "dtype" in _err(lib)
+    assert lib.mxf8_attn_quant_kv(d, st, None, st, 0, 1, 1, 16, 128, d, d, d, d, None, d, None) == 1 \
+        and "null" in _err(lib)
+    assert lib.mxf8_attn_quant_kv(d, st, d, st, 0, 1, 1, 16, 128, d, d, d, d, None, None, None) == 1 \
+        and "workspace" in _err(lib)
+    assert lib.mxf8_attn_quant_kv(d, st, d, st, 0, 1, 1, 0, 128, d, d, d, d, None, d, None) == 1
+    assert lib.mxf8_attn_kv_workspace_bytes(1, 24, 20280, 128) > 0
+    assert lib.mxf8_attn_kv_workspace_bytes(1, 0, 20280, 128) == 0

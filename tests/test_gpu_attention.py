@@ -67,6 +67,53 @@ def test_attention_quantizers_bit_exact(B, H, S, D, permuted, dtype):
     assert not codes(v8t)[..., S:].any()
 
 
+@pytest.mark.parametrize("B,H,S,D,layout,dtype", [
+    (2, 3, 333, 128, "packed", torch.bfloat16), (1, 2, 700, 128, "contig", torch.bfloat16),
+    (2, 2, 130, 64, "packed", torch.float16), (1, 3, 5, 128, "permuted", torch.bfloat16),
+    (1, 2, 256, 64, "strided", torch.bfloat16), (2, 24, 2600, 128, "packed", torch.bfloat16),
+])
+def test_attention_quant_kv_matches_separate_and_oracle(B, H, S, D, layout, dtype):
+    """attn_quant_kv (one pass for both statistics, one fold, one pass quantizing K and V)
+    equals attn_kmean + attn_quant_k + attn_quant_v bit for bit, and the oracle: V codes
+    and scales bit-exact, K codes and scales bit-exact given the kernel's own key mean, the
+    mean within 1e-6 of max|k|.  Layouts: K and V halves of one [B, S, 2, H, D] projection
+    (packed), contiguous, permuted [B, S, H, D] views, and a channel stride of 2 (strided)."""
+    _say(f"attn quant_kv B={B} H={H} S={S} D={D} {layout} {dtype}")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(S * 3 + D + B)
+    k, v = bf16_randn(rng, (B, H, S, D)), bf16_randn(rng, (B, H, S, D), 2.0)
+    k = bf16_round(k + bf16_randn(rng, (1, H, 1, D), 2.0))  # a non-zero key mean per head
+    if dtype == torch.float16:
+        k, v = (t.astype(np.float16).astype(np.float32) for t in (k, v))
+    if layout == "packed":
+        kv = np.ascontiguousarray(np.stack([k, v], 2).transpose(0, 3, 2, 1, 4))  # [B, S, 2, H, D]
+        g = to_gpu(kv, dtype)
+        kg, vg = g[:, :, 0].permute(0, 2, 1, 3), g[:, :, 1].permute(0, 2, 1, 3)
+    elif layout == "strided":
+        kg = to_gpu(np.repeat(k, 2, axis=-1), dtype)[..., ::2]
+        vg = to_gpu(np.repeat(v, 2, axis=-1), dtype)[..., ::2]
+        assert kg.stride(-1) == 2
+    else:
+        kg, vg = _layout(k, layout == "permuted", dtype), _layout(v, layout == "permuted", dtype)
+    k8, sk, v8t, sv, mu = ops.attn_quant_kv(kg, vg)
+    mu_s = ops.attn_kmean(kg)
+    k8s, sks = ops.attn_quant_k(kg, mu_s)
+    v8ts, svs = ops.attn_quant_v(vg)
+    assert torch.equal(mu, mu_s) and torch.equal(sk, sks) and torch.equal(sv, svs)
+    assert torch.equal(k8.view(torch.uint8), k8s.view(torch.uint8))
+    assert torch.equal(v8t.view(torch.uint8), v8ts.view(torch.uint8))
+    rmu = oa.key_mean(k)[:, :, 0, :]
+    assert np.abs(mu.cpu().numpy() - rmu).max() <= 1e-6 * np.abs(k).max()
+    rk8, rsk = oa.quantize_k(k, mu.cpu().numpy()[:, :, None, :])
+    np.testing.assert_array_equal(sk.cpu().numpy(), rsk)
+    np.testing.assert_array_equal(codes(k8)[:, :, :S], rk8)
+    assert not codes(k8)[:, :, S:].any()
+    rv8t, rsv = oa.quantize_v(v)
+    np.testing.assert_array_equal(sv.cpu().numpy(), rsv)
+    np.testing.assert_array_equal(codes(v8t)[..., :S], rv8t)
+    assert not codes(v8t)[..., S:].any()
+
+
 def _fwd_case(rng, B, H, Sq, Sk, D, mask=None, bias=None, tau=-1.0, permuted=False, dtype=torch.bfloat16):
     """Runs the GPU forward on the oracle's own codes/scales and compares outputs."""
     from minimaxh3_amd import ops

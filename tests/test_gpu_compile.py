@@ -83,7 +83,7 @@ def test_compiled_block_one_graph_same_result(fused_adaln):
             targets = {str(n.target) for g in ex.graphs for n in g.graph.nodes}
             # q is a view of the fused projection output, so the Q quantizer runs inside
             # the attention launch (mxf8.attn_fwd_q)
-            for op in ("mxf8.gemm_rowwise", "mxf8.attn_fwd_q", "mxf8.attn_quant_k", "mxf8.attn_quant_v"):
+            for op in ("mxf8.gemm_rowwise", "mxf8.attn_fwd_q", "mxf8.attn_quant_kv"):
                 assert any(op in t for t in targets), (op, sorted(targets))
             if fused_adaln:
                 assert any("mxf8.adaln_quant_rows" in t for t in targets)

@@ -166,6 +166,20 @@ int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], const void* v,
                        hipStream_t stream);
 
 /*
+ * mxf8_attn_quant_kv without a workspace argument and without any device allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its scratch is a 4 MiB device array inside the library (one copy per GPU, held until the
+ * process ends), enough for every B*H <= 1638 at D = 128 (<= 5461 at D = 64); larger shapes
+ * are rejected with MXF8_EINVAL before any launch.  Every call on one GPU shares that
+ * GPU's copy: calls that overlap on one GPU (other streams or threads) race.  Outputs are
+ * those of mxf8_attn_quant_kv bit for bit.
+ */
+int mxf8_attn_quant_kv_noalloc(const void* k, const int64_t k_strides[4], const void* v,
+                               const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                               uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean, hipStream_t stream);
+
+/*
  * FP8 flash-attention forward.  Replaces _fp8_attn_kernel (kernels/fp8_attention.py:185-297,
  * launch 380-402) with BLOCK_N = 128: log2-domain scores, staggered KV visit order, lazy
  * row max (moves only when the tile max exceeds it by more than 8), exp2-free e4m3 P codes,

@@ -41,6 +41,8 @@ _SIGNATURES = {
     "mxf8_attn_kv_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "mxf8_attn_quant_kv": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _vp]),
+    "mxf8_attn_quant_kv_noalloc": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                                          _vp, _vp]),
     "mxf8_attn_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i32, _I64x4, _i64, _i64, _i64, _i64,
                              _i64, _vp]),
     "mxf8_attn_fwd_q": (_i32, [_vp, _I64x4, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _i32, _I64x4, _i64,

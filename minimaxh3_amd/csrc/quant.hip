@@ -6,6 +6,9 @@
 // slabs in a fixed order, so results do not depend on scheduling).
 #include <stdarg.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 
 namespace mxf8 {
@@ -995,6 +998,72 @@ extern "C" int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], con
   const int64_t BH = B * H;
   const int nch = colreduce_chunks(BH, S);
   float* part = static_cast<float*>(workspace);
+  float* mean_ws = part + 2 * (int64_t)nch * BH * D;
+  return attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
+                            mean ? mean : mean_ws, part, nch, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// No-allocation form of mxf8_attn_quant_kv for callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+// Its workspace is a file-scope device array: each GPU the library runs on holds its own
+// copy until the process ends.  Host code never uses the array's name as an address: the
+// entry point's first call on a device (that device current) looks up the device's copy
+// with hipGetSymbolAddress and keeps it.  Every call on one GPU shares that GPU's copy, so
+// calls that overlap on one GPU (other streams, other threads) race.  Nothing in it needs
+// clearing: every partial slab and the key mean are written before they are read.
+// ---------------------------------------------------------------------------------------
+// 4 MiB: enough for every B*H <= 1638 at D = 128 (<= 5461 at D = 64)
+constexpr int64_t kNoAllocScratchBytes = (int64_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's copy of `scratch` (looked up once per device, with the device current).
+int scratch_ptr(const char* what, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(MXF8_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MXF8_EINVAL, "%s: device %d out of range", what, dev);
+  void* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_dev[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return set_error(MXF8_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", what, hipGetErrorString(e));
+      g_scratch_dev[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MXF8_OK;
+}
+}  // namespace
+
+extern "C" int mxf8_attn_quant_kv_noalloc(const void* k, const int64_t k_strides[4], const void* v,
+                                          const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S,
+                                          int64_t D, uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean,
+                                          hipStream_t stream) {
+  const char* what = "attn_quant_kv_noalloc";
+  int rc = attn_quant_kv_checks(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv);
+  if (rc) return rc;
+  const int64_t need = mxf8_attn_kv_workspace_bytes(B, H, S, D);
+  if (need > kNoAllocScratchBytes)
+    return set_error(MXF8_EINVAL,
+                     "%s: B*H=%lld, S=%lld, D=%lld need %lld bytes of scratch, more than its %lld (use "
+                     "mxf8_attn_quant_kv with a workspace)",
+                     what, (long long)(B * H), (long long)S, (long long)D, (long long)need,
+                     (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_ptr(what, &ws);
+  if (rc) return rc;
+  const int64_t BH = B * H;
+  const int nch = colreduce_chunks(BH, S);  // as mxf8_attn_quant_kv: the same sums, bit for bit
+  float* part = static_cast<float*>(ws);
   float* mean_ws = part + 2 * (int64_t)nch * BH * D;
   return attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
                             mean ? mean : mean_ws, part, nch, stream);

@@ -7,8 +7,12 @@ gfx950 HIP kernels of ``minimaxh3_amd`` (per-row e4m3 quantizer, row-wise scaled
 with the bias / LoRA / GELU-tanh epilogue fused); there is no fallback path.
 
 Differences from the reference that do not change results: no padding of M to a
-multiple of 16 (fp8_linear.py:91-93; the GEMM handles any M), and the LoRA branch of
-FP8Linear runs inside the GEMM epilogue instead of as separate bf16 matmuls + add.
+multiple of 16 (fp8_linear.py:91-93; the GEMM handles any M), and for bf16 inputs (the
+DiT's dtype) one LoRA adapter runs inside the GEMM epilogue with the reference's three bf16
+roundings instead of as separate bf16 matmuls + add.  Inputs of other dtypes apply their
+adapters after the GEMM exactly as the reference does, since its final add happens in the
+input's dtype; several adapters on bf16 inputs are concatenated along the rank, which
+rounds their summed branch once instead of once per adapter.
 """
 from __future__ import annotations
 
@@ -139,6 +143,14 @@ class FP8Linear(nn.Module):
         adapters = self.adapters
         if not adapters:
             return None, None, 0.0
+        xb = x2d if x2d.dtype == torch.bfloat16 else x2d.to(torch.bfloat16)
+        if torch.compiler.is_compiling():
+            # Traced (the reference compiles each block before LoRAs are appended,
+            # runtime/model_manager.py:127-141 and runtime/lora.py:263-302): the operands are
+            # built in the graph, which for one rank-aligned bf16 adapter is A and B as they
+            # stand; the compiler's guards on the adapter list replace the cache below.
+            a, b, scale = self._combine(adapters)
+            return ops.lora_down(xb, a), b, scale
         # the key holds the adapter tensors themselves (an id() of a freed tensor can be
         # reused) and their in-place version counters
         key = [(A, B, float(s), A._version, B._version) for A, B, s in adapters]
@@ -146,19 +158,24 @@ class FP8Linear(nn.Module):
         hit = old is not None and len(old) == len(key) and all(
             o[0] is k[0] and o[1] is k[1] and o[2:] == k[2:] for o, k in zip(old, key))
         if not hit:
-            if len(adapters) == 1:
-                A, B, scale = adapters[0]
-                a, b = self._pad_rank(A.to(torch.bfloat16), B.to(torch.bfloat16))
-            else:
-                a = torch.cat([A.to(torch.bfloat16) for A, _, _ in adapters], 0)
-                b = torch.cat([(B.float() * float(s)).to(torch.bfloat16) for _, B, s in adapters], 1)
-                a, b = self._pad_rank(a, b)
-                scale = 1.0
-            self._lora_cache = (a.contiguous(), b.contiguous(), float(scale))
+            self._lora_cache = self._combine(adapters)
             self._lora_cache_key = key
         a, b, scale = self._lora_cache
-        xb = x2d if x2d.dtype == torch.bfloat16 else x2d.to(torch.bfloat16)
         return ops.lora_down(xb, a), b, scale
+
+    @classmethod
+    def _combine(cls, adapters):
+        """(A, B, scale) of the fused epilogue: one adapter as it is, several concatenated
+        along the rank with each scale folded into its B; ranks zero-padded to 16."""
+        if len(adapters) == 1:
+            A, B, scale = adapters[0]
+            a, b = cls._pad_rank(A.to(torch.bfloat16), B.to(torch.bfloat16))
+        else:
+            a = torch.cat([A.to(torch.bfloat16) for A, _, _ in adapters], 0)
+            b = torch.cat([(B.float() * float(s)).to(torch.bfloat16) for _, B, s in adapters], 1)
+            a, b = cls._pad_rank(a, b)
+            scale = 1.0
+        return a.contiguous(), b.contiguous(), float(scale)
 
     @staticmethod
     def _pad_rank(A: torch.Tensor, B: torch.Tensor):
@@ -173,6 +190,15 @@ class FP8Linear(nn.Module):
         orig_shape = x.shape
         x2d = x.reshape(-1, self.in_features)
         x8, x_scale = quantize_rows(x2d)
+        if self.adapters and x.dtype != torch.bfloat16:
+            # The reference converts the bf16 linear output to x's dtype and adds each LoRA
+            # branch in that dtype (fp8_linear.py:105-108); the fused epilogue adds in bf16,
+            # so other dtypes take the reference's sequence (then the folded tanh-GELU).
+            out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, ACT_NONE, None, None, 0.0)
+            out = apply_lora_adapters(x2d, out.to(x.dtype), self.adapters)
+            if self.act == ACT_GELU_TANH:
+                out = torch.nn.functional.gelu(out, approximate="tanh")
+            return out.reshape(*orig_shape[:-1], self.out_features)
         lora_t, lora_b, lora_scale = self._lora_operands(x2d)
         out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
                                lora_scale)
@@ -183,8 +209,14 @@ class FP8Linear(nn.Module):
         """``forward`` on an input quantized already (``adaln_quantize_rows``): x8 [M, K] e4m3,
         x_scale [M, 1] fp32 -> bf16 [M, N].  LoRA adapters read the bf16 input
         ``x_modulated`` [M, K] (``return_modulated=True``), as in ``forward``."""
-        if x8.ndim != 2 or x8.shape[1] != self.in_features:
-            raise ValueError(f"forward_quantized: expected x8 [M, {self.in_features}]")
+        if x8.ndim != 2 or x8.shape[1] != self.in_features or x8.dtype != torch.float8_e4m3fn:
+            raise ValueError(f"forward_quantized: expected e4m3 x8 [M, {self.in_features}]")
+        if not x8.is_contiguous():
+            raise ValueError("forward_quantized: x8 must be contiguous")
+        M = x8.shape[0]
+        if (x_scale.dtype != torch.float32 or x_scale.numel() != M or x_scale.device != x8.device
+                or not x_scale.is_contiguous()):
+            raise ValueError(f"forward_quantized: x_scale must hold {M} contiguous fp32 scales on {x8.device}")
         lora_t = lora_b = None
         lora_scale = 0.0
         if self.adapters:

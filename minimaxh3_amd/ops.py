@@ -26,6 +26,35 @@ def _prep(t: torch.Tensor, what: str) -> None:
     N.require_gfx950(t.device)
 
 
+def _on(t: torch.Tensor | None, device: torch.device, what: str) -> None:
+    if t is not None and t.device != device:
+        raise ValueError(f"{what} must be on {device}, got {t.device}")
+
+
+def key_operands(key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, B: int, Sk: int,
+                 device: torch.device) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """The kernel's per-key operands: a mask as uint8 [B, Sk] (nonzero = keep, the truth value
+    of the reference's ``key_mask.to(torch.bool)``, fp8_attention.py:374) and a bias as fp32
+    [B, Sk] (375).  Either may hold B*Sk values or Sk values shared by every batch item; it
+    must be on the attention's device (ValueError otherwise)."""
+    out = []
+    for t, dt, name in ((key_mask, torch.bool, "key_mask"), (key_bias, torch.float32, "key_bias")):
+        if t is None:
+            out.append(None)
+            continue
+        _on(t, device, name)
+        t = t.to(dt)
+        if t.numel() == B * Sk:
+            t = t.reshape(B, Sk)
+        elif t.numel() == Sk:
+            t = t.reshape(1, Sk).expand(B, Sk)
+        else:
+            raise ValueError(f"{name} must hold B*Sk = {B * Sk} (or Sk = {Sk}) values, got shape {tuple(t.shape)}")
+        t = t.contiguous()
+        out.append(t.view(torch.uint8) if dt == torch.bool else t)
+    return out[0], out[1]
+
+
 # ---------------------------------------------------------------------------------------
 # FP8 linear
 # ---------------------------------------------------------------------------------------
@@ -106,6 +135,23 @@ def gemm_rowwise(a8: torch.Tensor, w8: torch.Tensor, sa: torch.Tensor, sw: torch
     _prep(a8, "gemm_rowwise")
     M, K = a8.shape
     Nn = w8.shape[0]
+    dev = a8.device
+    if a8.dtype != E4M3 or w8.dtype != E4M3 or w8.dim() != 2 or w8.shape[1] != K:
+        raise ValueError(f"gemm_rowwise: e4m3 a8 [M, K] and w8 [N, K] expected, got {a8.dtype} {tuple(a8.shape)} "
+                         f"and {w8.dtype} {tuple(w8.shape)}")
+    if not (a8.is_contiguous() and w8.is_contiguous()):
+        raise ValueError("gemm_rowwise: a8 and w8 must be contiguous")
+    if sa.dtype != torch.float32 or sa.numel() != M or sw.dtype != torch.float32 or sw.numel() != Nn:
+        raise ValueError(f"gemm_rowwise: fp32 scales of {M} rows and {Nn} channels expected")
+    if not (sa.is_contiguous() and sw.is_contiguous()):
+        raise ValueError("gemm_rowwise: scales must be contiguous")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != Nn or not bias.is_contiguous()):
+        raise ValueError(f"gemm_rowwise: bias must be {Nn} contiguous bf16 values")
+    if lora_t is not None and (lora_b is None or lora_t.shape[0] != M or lora_b.shape != (Nn, lora_t.shape[1])
+                               or not lora_t.is_contiguous() or not lora_b.is_contiguous()):
+        raise ValueError("gemm_rowwise: LoRA operands t [M, r] and B [N, r] (contiguous bf16) expected")
+    for t, name in ((w8, "w8"), (sa, "sa"), (sw, "sw"), (bias, "bias"), (lora_t, "lora_t"), (lora_b, "lora_b")):
+        _on(t, dev, f"gemm_rowwise: {name}")
     out = torch.empty((M, Nn), dtype=torch.bfloat16, device=a8.device)
     if M == 0 or Nn == 0:
         return out
@@ -287,8 +333,7 @@ def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Te
     _prep(q8, "attn_fwd")
     B, H, Sq, D = like.shape
     out = torch.empty_like(like)
-    km = None if key_mask is None else key_mask.to(torch.uint8).contiguous()
-    kb = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    km, kb = key_operands(key_mask, key_bias, B, Sk, q8.device)
     with torch.cuda.device(q8.device):
         N.check(N.load().mxf8_attn_fwd(
             q8.data_ptr(), k8.data_ptr(), v8t.data_ptr(), sq.data_ptr(), sk.data_ptr(), sv.data_ptr(),
@@ -327,8 +372,7 @@ def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, s
         return attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, q, Sk)
     B, H, Sq, D = q.shape
     out = torch.empty_like(q)
-    km = None if key_mask is None else key_mask.to(torch.uint8).contiguous()
-    kb = None if key_bias is None else key_bias.to(torch.float32).contiguous()
+    km, kb = key_operands(key_mask, key_bias, B, Sk, q.device)
     with torch.cuda.device(q.device):
         N.check(N.load().mxf8_attn_fwd_q(
             q.data_ptr(), N.strides4(q), float(c), k8.data_ptr(), v8t.data_ptr(), sk.data_ptr(), sv.data_ptr(),

@@ -66,35 +66,52 @@ def gelu_tanh(z):
     return (0.5 * z * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (z + 0.044715 * z ** 3)))).astype(F32)
 
 
-def lora_branch_add(x, out, adapters):
+def _round_to(dtype):
+    """Rounding to the stored dtype of an output: "bf16" or "fp16" (values kept as fp32)."""
+    if dtype == "bf16":
+        return bf16_round
+    if dtype == "fp16":
+        return lambda a: np.asarray(a, F32).astype(np.float16).astype(F32)
+    raise ValueError(dtype)
+
+
+def lora_branch_add(x, out, adapters, out_dtype="bf16"):
     """apply_lora_adapters (fp8_linear.py:45-55) with torch's bf16 matmul rounding.
 
-    For each (A [r,K], B [N,r], scale): out = bf16(out + bf16(bf16(bf16(x@A^T) @ B^T) * scale)).
-    x, A, B are bf16-valued fp32 arrays; matmuls accumulate in float64 then round to bf16.
+    For each (A [r,K], B [N,r], scale): branch = bf16(bf16(bf16(x@A^T) @ B^T) * scale) (x is
+    converted to A's dtype, bf16, line 53), converted to out's dtype and added in it (line 54):
+    out = r(out + r(branch)) with r the rounding to ``out_dtype`` (bf16 or fp16; the linear
+    output reaches that dtype through ``.to(x.dtype)``, line 107).  x, A, B are fp32 arrays;
+    matmuls accumulate in float64 then round to bf16.
     """
-    out = bf16_round(out)
+    rnd = _round_to(out_dtype)
+    out = rnd(out)
     x = bf16_round(x).astype(np.float64)
     for A, B, scale in adapters:
         t = bf16_round((x @ np.asarray(A, np.float64).T).astype(F32))
         branch = bf16_round((t.astype(np.float64) @ np.asarray(B, np.float64).T).astype(F32))
         branch = bf16_round((branch * F32(scale)).astype(F32))
-        out = bf16_round((out + branch).astype(F32))
+        out = rnd((out + rnd(branch)).astype(F32))
     return out
 
 
-def fp8_linear_forward(x, w8, w_scale, bias=None, adapters=(), gelu=False):
-    """FP8Linear.forward (fp8_linear.py:87-108) on [M, K] inputs, bf16 result as fp32.
+def fp8_linear_forward(x, w8, w_scale, bias=None, adapters=(), gelu=False, in_dtype="bf16"):
+    """FP8Linear.forward (fp8_linear.py:87-108) on [M, K] inputs of ``in_dtype`` (bf16 or fp16
+    values), the result as fp32 holding values of that dtype.
 
     Padding M to a multiple of 16 (lines 91-93) only adds zero rows whose outputs are
-    sliced away (line 106), so it does not change any kept value and is not modelled.
-    ``gelu`` applies the tanh-GELU of the following FFN activation after the LoRA add.
+    sliced away (line 106), so it does not change any kept value and is not modelled.  The
+    bf16 linear output is converted to the input's dtype (line 107) before the LoRA adds.
+    ``gelu`` applies the tanh-GELU of the following FFN activation after the LoRA add, rounded
+    to that dtype.
     """
-    x = bf16_round(np.asarray(x, F32))
+    rnd = _round_to(in_dtype)
+    x = rnd(np.asarray(x, F32))
     x8, sa = quantize_rows(x)
-    out = bf16_round(scaled_mm(x8, w8, sa, w_scale, bias))
-    out = lora_branch_add(x, out, adapters) if adapters else out
+    out = rnd(bf16_round(scaled_mm(x8, w8, sa, w_scale, bias)))
+    out = lora_branch_add(x, out, adapters, in_dtype) if adapters else out
     if gelu:
-        out = bf16_round(gelu_tanh(out))
+        out = rnd(gelu_tanh(out))
     return out
 
 

@@ -515,3 +515,31 @@ def test_forward_quantized_equals_forward(fl, lora):
     if lora:
         with pytest.raises(ValueError):
             mod.forward_quantized(x8, sa)
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_fp16_input_lora_follows_reference_sequence(fl, gelu):
+    """fp16 activations with a LoRA adapter: the bf16 linear output is converted to fp16 and
+    the branch added in fp16, as the reference does (fp8_linear.py:105-108), then the folded
+    tanh-GELU in fp16; against the oracle's fp16 statement at the GEMM bar."""
+    _say(f"fp16 input LoRA gelu={gelu}")
+    rng = np.random.default_rng(21)
+    M, K, N, r = 300, 512, 384, 32
+    x = with_outliers(rng, bf16_randn(rng, (M, K))).astype(np.float16).astype(np.float32)
+    w, b = bf16_randn(rng, (N, K), 0.02), bf16_randn(rng, (N,), 0.01)
+    A, B = bf16_randn(rng, (r, K), 0.08), bf16_randn(rng, (N, r), 0.08)
+    lin = torch.nn.Linear(K, N, bias=True).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(w))
+        lin.bias.copy_(to_gpu(b))
+    mod = fl.FP8Linear.from_linear(lin)
+    mod.act = 1 if gelu else 0
+    mod.adapters.append((to_gpu(A), to_gpu(B), 0.75))
+    out = mod(to_gpu(x, torch.float16))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.shape == (M, N)
+    w8c, swc = ol.quantize_rows(w)
+    ref = ol.fp8_linear_forward(x, w8c, swc, b, adapters=[(A, B, 0.75)], gelu=gelu, in_dtype="fp16")
+    assert_gemm_close(out.float().cpu().numpy(), ref)
+    no_lora = ol.fp8_linear_forward(x, w8c, swc, b, gelu=gelu, in_dtype="fp16")
+    assert np.abs(ref - no_lora).max() > 5e-2 * np.abs(ref).max()

@@ -271,3 +271,89 @@ def test_from_quantized_validates():
     with pytest.raises(ValueError):
         fl.FP8Linear.from_quantized(codes, torch.ones(32, dtype=torch.float64))
     np.testing.assert_array_equal(m.w8.view(torch.uint8).numpy(), np.zeros((32, 16), np.uint8))
+
+
+def test_checkpoint_fingerprint_refuses_stale_codes(stub, tmp_path):
+    """A cache keyed by the conversion fingerprint: a load expecting another fingerprint (other
+    fused LoRAs, exclude patterns, kept edge blocks or base weights) is refused untouched."""
+    fp = ck.conversion_fingerprint("to_k,norm", 1, fused_loras=[("lora_a.safetensors", 0.8)], source="rev1")
+    assert fp == ck.conversion_fingerprint(["norm", " to_k"], 1, [("lora_a.safetensors", 0.8)], "rev1")
+    others = [ck.conversion_fingerprint("to_k", 1, [("lora_a.safetensors", 0.8)], "rev1"),
+              ck.conversion_fingerprint("to_k,norm", 2, [("lora_a.safetensors", 0.8)], "rev1"),
+              ck.conversion_fingerprint("to_k,norm", 1, [("lora_a.safetensors", 0.9)], "rev1"),
+              ck.conversion_fingerprint("to_k,norm", 1, [("lora_a.safetensors", 0.8)], "rev2"),
+              ck.conversion_fingerprint("to_k,norm", 1, [("lora_a.safetensors", 0.8)], "rev1", fuse_gelu=True)]
+    assert len({fp, *others}) == 6
+    conv = Toy()
+    fl.convert_transformer_to_fp8(conv, "", keep_edge_blocks=1)
+    path = str(tmp_path / "fp8.safetensors")
+    ck.save_fp8_checkpoint(conv, path, fingerprint=fp)
+    fresh = Toy()
+    with pytest.raises(ValueError, match="fingerprint"):
+        ck.load_fp8_checkpoint(fresh, path, device="cpu", fingerprint=others[0])
+    assert not _converted_paths(fresh)
+    assert ck.load_fp8_checkpoint(fresh, path, device="cpu", fingerprint=fp) == 24
+    # a file saved without a fingerprint does not satisfy a load that expects one
+    plain = str(tmp_path / "plain.safetensors")
+    ck.save_fp8_checkpoint(conv, plain)
+    with pytest.raises(ValueError, match="fingerprint"):
+        ck.load_fp8_checkpoint(Toy(), plain, device="cpu", fingerprint=fp)
+
+
+def test_checkpoint_tensor_and_bias_checks_run_before_any_change(stub, tmp_path):
+    """Missing tensors, wrong stored dtypes and a bias the target lacks (or has) are refused in
+    the first pass: the transformer is left as it was."""
+    from safetensors import safe_open
+    conv = Toy()
+    fl.convert_transformer_to_fp8(conv, "", keep_edge_blocks=0)
+    path = str(tmp_path / "fp8.safetensors")
+    ck.save_fp8_checkpoint(conv, path)
+    with safe_open(path, framework="pt") as f:
+        meta = f.metadata()
+        tensors = {k: f.get_tensor(k) for k in f.keys()}
+    last = "blocks.5.attn.to_out.0"
+
+    def variant(name, edit):
+        t = dict(tensors)
+        edit(t)
+        p = str(tmp_path / name)
+        save_file(t, p, metadata=meta)
+        return p
+
+    cases = [
+        (variant("nobias.safetensors", lambda t: t.pop(f"{last}.bias")), "missing"),
+        (variant("f16scale.safetensors", lambda t: t.update({f"{last}.w_scale": t[f"{last}.w_scale"].half()})),
+         "w_scale"),
+        (variant("u8codes.safetensors", lambda t: t.update({f"{last}.w8": t[f"{last}.w8"].view(torch.uint8)})),
+         "w8"),
+    ]
+    for p, msg in cases:
+        fresh = Toy()
+        with pytest.raises(ValueError, match=msg):
+            ck.load_fp8_checkpoint(fresh, p, device="cpu")
+        assert not _converted_paths(fresh), p
+    # the target linear lacks the stored bias (or has one the file lacks)
+    nob = Toy()
+    nob.blocks[5].attn.to_out[0] = nn.Linear(D, D, bias=False)
+    with pytest.raises(ValueError, match="bias"):
+        ck.load_fp8_checkpoint(nob, path, device="cpu")
+    assert not _converted_paths(nob)
+    conv_k = Toy()  # to_k has no bias in Toy: give the target one
+    conv_k.blocks[0].attn.to_k = nn.Linear(D, D, bias=True)
+    with pytest.raises(ValueError, match="bias"):
+        ck.load_fp8_checkpoint(conv_k, path, device="cpu")
+    assert not _converted_paths(conv_k)
+
+
+def test_forward_quantized_validates_operands():
+    codes8 = torch.zeros((32, 16), dtype=torch.uint8).view(torch.float8_e4m3fn)
+    m = fl.FP8Linear.from_quantized(codes8, torch.ones(32), None, "cpu")
+    x8 = torch.zeros((5, 16), dtype=torch.uint8).view(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="x_scale"):
+        m.forward_quantized(x8, torch.ones(4, 1))
+    with pytest.raises(ValueError, match="x_scale"):
+        m.forward_quantized(x8, torch.ones(5, 1, dtype=torch.float64))
+    with pytest.raises(ValueError, match="e4m3"):
+        m.forward_quantized(x8.view(torch.uint8), torch.ones(5, 1))
+    with pytest.raises(ValueError, match="contiguous"):
+        m.forward_quantized(torch.zeros((16, 5), dtype=torch.uint8).view(torch.float8_e4m3fn).t(), torch.ones(5, 1))

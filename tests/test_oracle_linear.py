@@ -87,6 +87,27 @@ def test_lora_branch_matches_torch_bf16():
     np.testing.assert_allclose(got, ref, rtol=2 ** -7, atol=1e-6)
 
 
+def test_lora_branch_fp16_output_matches_torch():
+    """fp16 inputs: the reference converts the bf16 linear output to fp16 and adds each bf16
+    branch after converting it to fp16 (fp8_linear.py:54, 107)."""
+    rng = np.random.default_rng(4)
+    M, K, N, r = 24, 64, 48, 8
+    x = (rng.standard_normal((M, K))).astype(np.float16).astype(np.float32)
+    out = _bf16_randn(rng, (M, N))
+    A = _bf16_randn(rng, (r, K), 0.05)
+    B = _bf16_randn(rng, (N, r), 0.05)
+    got = lora_branch_add(x, out, [(A, B, 0.75)], out_dtype="fp16")
+    assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+    xt, ot = torch.from_numpy(x).half(), torch.from_numpy(out).bfloat16().to(torch.float16)
+    At, Bt = torch.from_numpy(A).bfloat16(), torch.from_numpy(B).bfloat16()
+    branch = (xt.to(torch.bfloat16) @ At.t()) @ Bt.t()
+    ref = (ot + (branch * 0.75).to(torch.float16)).float().numpy()
+    # torch's CPU bf16 matmul may accumulate in a different order: one bf16 ulp of the branch
+    np.testing.assert_allclose(got, ref, rtol=2 ** -7, atol=1e-6)
+    # and the sum is taken in fp16: it differs from the bf16 statement of the same branch
+    assert not np.array_equal(got, lora_branch_add(x, out, [(A, B, 0.75)]))
+
+
 # ------------------------------------------------------------------ adaLN modulation
 
 def _bf16_ulp_diff(a, b):

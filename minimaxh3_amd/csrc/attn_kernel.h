@@ -503,12 +503,21 @@ __device__ __forceinline__ bool attn_tile_needs_mask(const uint8_t* sAux, int kv
   }
 }
 
+// S = (dot * sq) * sk + bias * log2(e) with every operation rounded on its own, as the
+// reference's statements are (kernels/fp8_attention.py:253, 259).  Contraction is off here:
+// an FMA that one kernel forms and another does not would move S by an ulp, which decides
+// ties of the code's rounding, so that kernels of the same arithmetic would not give the
+// same bits.
+__device__ __forceinline__ float attn_bias_score(float dot, float sq, float skj, float bias) {
+#pragma clang fp contract(off)
+  return (dot * sq) * skj + bias * 1.4426950408889634f;
+}
+
 // Invalid keys (past Sk, masked, bias <= -1e8) get attn_invalid_score; with a bias S is
 // formed explicitly as (dot * sq) * sk + bias * log2 e.
 template <bool HAS_MASK, bool HAS_BIAS>
 __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sAux, int kv0, int Sk, float sq,
                                                  float skj, int lane) {
-  constexpr float LOG2E_F = 1.4426950408889634f;
   const int g = lane >> 5;
   const float vinv = attn_invalid_score<HAS_BIAS>(sq, skj);
 #pragma unroll
@@ -533,7 +542,7 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
       float v = s[t][i];
       if constexpr (HAS_BIAS) {
         ok = ok && (bias[i] > -1.0e8f);
-        v = (v * sq) * skj + bias[i] * LOG2E_F;
+        v = attn_bias_score(v, sq, skj, bias[i]);
       }
       if constexpr (HAS_MASK) ok = ok && (((mbytes[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0u);
       s[t][i] = ok ? v : vinv;
@@ -564,11 +573,11 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
 // PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
 // significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
 // lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
-template <bool HAS_BIAS, bool REP>
-__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, float tau,
-                                            AttnPB<REP>& pb) {
-  // row max (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic), as four
-  // independent v_max3 chains so that the VALU need not wait on each result
+// Row max of the tile (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic)
+// and the lazy-max decision; returns the new row max m_new of the lane's query.  Four
+// independent v_max3 chains, so that the VALU need not wait on each result.
+template <bool HAS_BIAS>
+__device__ __forceinline__ float attn_tile_max(const v16f (&s)[4], float sq, float skj, float m_old) {
   float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -582,55 +591,99 @@ __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float 
     mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   }
   const float rmax = fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
-  const float m_new = (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
+  return (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
+}
 
-  const float cst = 56.0f - 8.0f * m_new;
-  const float c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
-  const float c8f = c8 * 0x1p64f;
-  const float cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
+// Per-tile constants of the code arithmetic (see attn_codes_sub).
+struct AttnCodeK {
+  float c8, cst, c8f, cstf, tau;
+  template <bool HAS_BIAS>
+  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float m_new, float tau) {
+    AttnCodeK k;
+    k.cst = 56.0f - 8.0f * m_new;
+    k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
+    k.c8f = k.c8 * 0x1p64f;
+    k.cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
+    k.tau = tau;
+    return k;
+  }
+};
+
+// The exp2-free P codes of score subtile t (the PV B operand words 4 (t & 1) .. + 3 of half
+// t >> 1).
+//
+// code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
+// 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
+// inactive.  Three FMAs per score, all at the full FMA rate:
+//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
+//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
+//   t    = fma(bits, keep, 1.5 * 2^23)
+// keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
+// is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
+// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
+// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
+// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
+//
+// Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
+// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
+// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
+// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
+// hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
+// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
+// significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
+// lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
+template <bool REP>
+__device__ __forceinline__ void attn_codes_sub(const v16f& st, const AttnCodeK& k, int t, AttnPB<REP>& pb) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int w4 = 0; w4 < 4; ++w4) {
+    uint32_t tb[4];
+    float bits[4];
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4) {
-      uint32_t tb[4];
-      float bits[4];
+    for (int e = 0; e < 4; ++e) {
+      const float x = st[4 * w4 + e];
+      bits[e] = __builtin_fmaf(x, k.c8, k.cst);
+      const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, k.c8f, k.cstf), 0.0f, 1.0f);
+      tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
+    }
+    // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
+    const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
+                          __builtin_amdgcn_perm(tb[3], tb[2], 0x04000c0cu);
+    // An empty use keeps the codes here instead of letting them sink to their consumer
+    // (the PV products): a reordered tile would hold the scores and the codes live together.
+    asm volatile("" ::"v"(word));
+    pb.p[t >> 1][4 * (t & 1) + w4] = (int)word;
+    if constexpr (REP) {
+      const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+      const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
+      const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
+      float d8[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float x = s[t][4 * w4 + e];
-        bits[e] = __builtin_fmaf(x, c8, cst);
-        const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, c8f, cstf), 0.0f, 1.0f);
-        tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
+        // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
+        const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
+        const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
+        d8[e] = papx[e] >= k.tau ? d : 0.0f;
       }
-      // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
-      const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
-                            __builtin_amdgcn_perm(tb[3], tb[2], 0x04000c0cu);
-      // An empty use keeps the codes here instead of letting them sink to their consumer
-      // (the PV products, which the ping-pong kernel issues in another phase).
-      asm volatile("" ::"v"(word));
-      pb.p[t >> 1][4 * (t & 1) + w4] = (int)word;
-      if constexpr (REP) {
-        const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
-        const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
-        const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
-        float d8[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
-          const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
-          const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
-          d8[e] = papx[e] >= tau ? d : 0.0f;
-        }
-        int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
-        hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
-        const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-        const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-        int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
-        lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
-        pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
-        pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
-      }
+      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
+      const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+      const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
+      pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
+      pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
     }
   }
+}
+
+// Row max, lazy-max decision and the codes of the whole tile; returns m_new.
+template <bool HAS_BIAS, bool REP>
+__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, float tau,
+                                            AttnPB<REP>& pb) {
+  const float m_new = attn_tile_max<HAS_BIAS>(s, sq, skj, m_old);
+  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, m_new, tau);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) attn_codes_sub<REP>(s[t], k, t, pb);
   return m_new;
 }
 

@@ -360,7 +360,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
             float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              v[e] = acc[a][b][4 * q + e] * sam * swq[e] + bq[e];
+              v[e] = __builtin_fmaf(acc[a][b][4 * q + e] * sam, swq[e], bq[e]);
               if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(bf16r(v[e]));
             }
             const int chunk = 4 * a + q;
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
             float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              v[e] = acc[a][b][4 * q + e] * sam * swq[q][e] + bq[q][e];
+              v[e] = __builtin_fmaf(acc[a][b][4 * q + e] * sam, swq[q][e], bq[q][e]);
               // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch *
               // scale, bf16 sum; GELU-tanh acts on the bf16 result
               if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);

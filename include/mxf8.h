@@ -29,6 +29,9 @@ enum { MXF8_BF16 = 0, MXF8_F16 = 1, MXF8_F32 = 2 };
 enum { MXF8_ACT_NONE = 0, MXF8_ACT_GELU_TANH = 1 };
 /* status codes */
 enum { MXF8_OK = 0, MXF8_EINVAL = 1, MXF8_ELAUNCH = 2 };
+/* kv_mode of the attention forward: AUTO holds each head's K/V in LDS when they fit, STREAM
+ * always streams K/V tiles (same bits either way) */
+enum { MXF8_ATTN_KV_AUTO = 0, MXF8_ATTN_KV_STREAM = 1 };
 
 /* Version of this ABI (major * 100 + minor). */
 int mxf8_abi_version(void);
@@ -187,16 +190,16 @@ int mxf8_attn_quant_kv_noalloc(const void* k, const int64_t k_strides[4], const 
  *   key_mask [B, Sk] uint8 (nonzero = keep) or NULL; key_bias [B, Sk] fp32 natural-log
  *   additive bias or NULL (entries <= -1e8 mask the key).
  *   out [B, H, Sq, D] of out_dtype (bf16/fp16) with element strides out_strides[4].
- *   Fully masked rows give 0.  Short key sequences (Sk <= 512 at D = 128, <= 1024 at
- *   D = 64) without repair run a kernel that holds each head's K/V in LDS; same bits
- *   (MXF8_ATTN_RESIDENT_KV=0 in the environment selects the streaming kernel).
+ *   Fully masked rows give 0.  kv_mode MXF8_ATTN_KV_AUTO: short key sequences (Sk <= 512
+ *   at D = 128, <= 1024 at D = 64) without repair run a kernel that holds each head's K/V
+ *   in LDS; MXF8_ATTN_KV_STREAM always streams K/V tiles.  Both give the same bits.
  */
 int mxf8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t,
                   const float* sq, const float* sk, const float* sv,
                   const uint8_t* key_mask, const float* key_bias, float repair_tau,
                   void* out, int out_dtype, const int64_t out_strides[4],
                   int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
-                  hipStream_t stream);
+                  int kv_mode, hipStream_t stream);
 
 /*
  * Q quantizer fused into the attention forward: _quantize_q_kernel + _fp8_attn_kernel
@@ -214,7 +217,7 @@ int mxf8_attn_fwd_q(const void* q, const int64_t q_strides[4], float c,
                     const uint8_t* key_mask, const float* key_bias, float repair_tau,
                     float* sq_out, void* out, int out_dtype, const int64_t out_strides[4],
                     int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
-                    hipStream_t stream);
+                    int kv_mode, hipStream_t stream);
 
 #ifdef __cplusplus
 }

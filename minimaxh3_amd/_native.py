@@ -17,6 +17,7 @@ _lib = None
 
 BF16, F16, F32 = 0, 1, 2
 ACT_NONE, ACT_GELU_TANH = 0, 1
+KV_AUTO, KV_STREAM = 0, 1
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -44,9 +45,9 @@ _SIGNATURES = {
     "mxf8_attn_quant_kv_noalloc": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                           _vp, _vp]),
     "mxf8_attn_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i32, _I64x4, _i64, _i64, _i64, _i64,
-                             _i64, _vp]),
+                             _i64, _i32, _vp]),
     "mxf8_attn_fwd_q": (_i32, [_vp, _I64x4, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _i32, _I64x4, _i64,
-                               _i64, _i64, _i64, _i64, _vp]),
+                               _i64, _i64, _i64, _i64, _i32, _vp]),
 }
 EXPORTS = tuple(_SIGNATURES)
 
@@ -59,27 +60,25 @@ def lib_path() -> str:
     return _LIB_PATH
 
 
-def load(path: str | None = None):
-    """Load libmxf8.so (idempotent) and attach the argument types of every export.
+def _bind(path: str):
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
 
-    With `path`, that library is loaded and becomes the one every later load() returns.
-    """
+
+def load():
+    """Load the in-tree libmxf8.so once (idempotent) with the argument types of every export."""
     global _lib
     with _lock:
-        if _lib is not None and path is None:
-            return _lib
-        p = path or _LIB_PATH
-        if not os.path.exists(p):
-            raise RuntimeError(
-                f"{p} is missing: build the HIP library first (python -m minimaxh3_amd.build)")
-        lib = ctypes.CDLL(p)
-        for name, (res, args) in _SIGNATURES.items():
-            fn = getattr(lib, name)
-            fn.restype = res
-            fn.argtypes = args
-        # an explicit path replaces the process-wide library: every later load() returns it
-        _lib = lib
-        return lib
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise RuntimeError(
+                    f"{_LIB_PATH} is missing: build the HIP library first (python -m minimaxh3_amd.build)")
+            _lib = _bind(_LIB_PATH)
+        return _lib
 
 
 def check(rc: int, what: str) -> None:

@@ -16,6 +16,6 @@
 namespace mxf8 {
 MXF8_ATTN_DECL_X(MXF8_ATTN_D, MXF8_ATTN_ODT) {
   attn_dispatch_flags<MXF8_ATTN_D, MXF8_ATTN_ODT>(hm, hb, rep, q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os, B, H, Sq,
-                                                   Sk, qa, st);
+                                                   Sk, qa, kv_mode, st);
 }
 }  // namespace mxf8

@@ -39,8 +39,6 @@
 // fragments three products ahead.
 #pragma once
 
-#include <stdlib.h>
-
 #include "common.h"
 
 namespace mxf8 {
@@ -168,32 +166,38 @@ struct AttnCtx {
   template <int QDT>
   __device__ __forceinline__ void quant_q(const AttnQ16& qa, int Sq, int nq, float* red) {
     uint4 raw[D / 64][4];
-    load_q16(qa, b, h, qrow < Sq ? qrow : -1, lane, raw);
-    quant_q_raw<QDT>(raw, qa, nq, red);
+    load_q16(qa, b, h, qrow, Sq, lane, raw);
+    quant_q_raw<QDT>(raw, qrow < Sq, qa, nq, red);
   }
 
   // The 16-bit Q values this lane quantizes: row `row` of head (b_, h_), bytes
-  // [64 hh + 32 g, +32) of its codes; row < 0 loads nothing (zeros).
-  static __device__ __forceinline__ void load_q16(const AttnQ16& qa, int b_, int h_, int row, int lane_,
+  // [64 hh + 32 g, +32) of its codes.  A row >= Sq reads row Sq - 1 and quant_q_raw is told
+  // to take zeros instead: the loads stay unconditional and nothing touches their
+  // registers before they are consumed, so no wait lands where they are issued and no
+  // branch splits the count of loads in flight that later waits rely on.
+  static __device__ __forceinline__ void load_q16(const AttnQ16& qa, int b_, int h_, int row, int Sq, int lane_,
                                                   uint4 (&raw)[D / 64][4]) {
     const int g = lane_ >> 5;
-    const uint16_t* qp = qa.q + (int64_t)b_ * qa.sb + (int64_t)h_ * qa.sh + (int64_t)row * qa.ss + 32 * g;
+    const uint16_t* qp =
+        qa.q + (int64_t)b_ * qa.sb + (int64_t)h_ * qa.sh + (int64_t)(row < Sq ? row : Sq - 1) * qa.ss + 32 * g;
 #pragma unroll
     for (int hh = 0; hh < D / 64; ++hh)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        raw[hh][u] = row >= 0 ? *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) raw[hh][u] = *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u);
   }
 
+  // valid = false: the row lies past Sq and quantizes as zeros.
   template <int QDT>
-  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], const AttnQ16& qa, int nq, float* red) {
+  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], bool valid, const AttnQ16& qa, int nq,
+                                              float* red) {
     float f[D / 64][32];
     float amax = 0.0f;
 #pragma unroll
     for (int hh = 0; hh < D / 64; ++hh)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t w[4] = {raw[hh][u].x, raw[hh][u].y, raw[hh][u].z, raw[hh][u].w};
+        const uint4 r = raw[hh][u];
+        const uint32_t w[4] = {valid ? r.x : 0u, valid ? r.y : 0u, valid ? r.z : 0u, valid ? r.w : 0u};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           f[hh][8 * u + 2 * i] = Elem<QDT>::lo(w[i]) * qa.c;
@@ -687,11 +691,36 @@ __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float 
   return m_new;
 }
 
+// The channel scales sv of head bh that this lane's output channels take (see attn_store).
+// They are loaded, and every load in flight waited for, before the first output store:
+// loads and stores retire in order, so a load still in flight behind a store would make
+// any later wait for it wait for the store as well.
+template <int D>
+struct AttnSv {
+  v4f r[D / 32][4];
+  __device__ __forceinline__ void load(const float* sv, int bh, int lane) {
+    const float* svh = sv + (int64_t)bh * D + 4 * (lane >> 5);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) r[dt][q4] = *reinterpret_cast<const v4f*>(svh + 32 * dt + 8 * q4);
+    wait_vm0();
+  }
+  // from a copy of the head's D scales in LDS
+  __device__ __forceinline__ void load_lds(const float* svl, int lane) {
+    const float* s = svl + 4 * (lane >> 5);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) r[dt][q4] = *reinterpret_cast<const v4f*>(s + 32 * dt + 8 * q4);
+  }
+};
+
 // O = (O + O_r) * sv / max(l, 1e-12) -> out (bf16 / fp16 through its strides; O_r is inside
 // O).  The lane holds query qrow, channels 32 dt + 8 (i/4) + 4 g + i%4.
 template <int D, int ODT>
-__device__ __forceinline__ void attn_store(const AttnState<D>& st, const float* sv, int bh, int b, int h,
-                                           int qrow, int lane, void* out, int64_t os_b, int64_t os_h, int64_t os_s,
+__device__ __forceinline__ void attn_store(const AttnState<D>& st, const AttnSv<D>& svr, int b, int h, int qrow,
+                                           int lane, void* out, int64_t os_b, int64_t os_h, int64_t os_s,
                                            int64_t os_d) {
   constexpr int NDT = D / 32;
   const int g = lane >> 5;
@@ -703,28 +732,35 @@ __device__ __forceinline__ void attn_store(const AttnState<D>& st, const float* 
   // (acc * sv) / den correctly rounded from one reciprocal per row (div_by_scale: the
   // quotients are O's values and den lies in [1e-12, ~1e7], so nothing over- or underflows)
   const float rden = __fdiv_rn(1.0f, den);
-  const float* svh = sv + (int64_t)bh * D;
   char* obase = static_cast<char*>(out) + ((int64_t)b * os_b + (int64_t)h * os_h + (int64_t)qrow * os_s) * 2;
+  // channels d0 .. d0 + 3 of chunk (dt, q4) as two packed 16-bit pairs
+  uint32_t ob[NDT][4][2];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const int d0 = 32 * dt + 8 * q4 + 4 * g;
-      const v4f sv4 = *reinterpret_cast<const v4f*>(svh + d0);
-      uint32_t ob[4];
+      float v[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = div_by_scale(st.o[dt][4 * q4 + e] * sv4[e], den, rden);
-        ob[e] = ODT == MXF8_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
-      }
-      uint16_t* dst = reinterpret_cast<uint16_t*>(obase) + (int64_t)d0 * os_d;
-      if (os_d == 1) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(int64_t)e * os_d] = (uint16_t)ob[e];
-      }
+      for (int e = 0; e < 4; ++e) v[e] = div_by_scale(st.o[dt][4 * q4 + e] * svr.r[dt][q4][e], den, rden);
+      ob[dt][q4][0] = cvt_pk_16<ODT>(v[0], v[1]);
+      ob[dt][q4][1] = cvt_pk_16<ODT>(v[2], v[3]);
     }
+  uint16_t* orow = reinterpret_cast<uint16_t*>(obase);
+  if (os_d == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * q4 + 4 * g) = make_uint2(ob[dt][q4][0], ob[dt][q4][1]);
+  } else {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        uint16_t* dst = orow + (int64_t)(32 * dt + 8 * q4 + 4 * g) * os_d;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(int64_t)e * os_d] = (uint16_t)(ob[dt][q4][e >> 1] >> (16 * (e & 1)));
+      }
   }
 }
 
@@ -764,7 +800,7 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
   for (int i = 0; i < nk; ++i) {
     // Tile i is the only DMA in flight; after the barrier every wave has finished tile
     // i-1, so its buffer can take tile i+1 while tile i is computed.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vm0();
     attn_barrier();
     const int jn = j + 1 == nk ? 0 : j + 1;
     if (i + 1 < nk) {
@@ -787,37 +823,46 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
   }
+  AttnSv<D> svr;
+  svr.load(sv, cx.bh, lane);
   if (cx.qrow >= Sq) return;
-  attn_store<D, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+  attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
 }
 
 // ---------------------------------------------------------------------------------------
 // Short key sequences (all KV tiles of a head fit in LDS: Sk <= 512 at D = 128, <= 1024 at
-// D = 64), Q from q8 / sq.  One persistent workgroup of 8 waves per CU walks a contiguous
-// range of (head, Q tile) work items; the head's K, V^T (and mask / bias) tiles are copied
-// into LDS once per head, and the two 4-wave groups take the range's Q tiles in pairs with
-// no barrier between heads.  Per Q tile the arithmetic and the KV visit order are those of
-// attn_fwd_kernel, so the output is the same bit for bit; what goes away is the per-tile
-// copy and barrier and the per-workgroup start-up, which dominate when a Q tile has only a
-// few KV tiles.  No repair path and no fused Q quantizer (its block amax would hold the two
-// groups in lockstep): the launcher uses attn_fwd_kernel for those.
+// D = 64).  One persistent workgroup of 8 waves per CU walks a contiguous range of (head,
+// Q tile) work items; the head's K, V^T (and mask / bias) tiles are copied into LDS once per
+// head, and the two 4-wave groups take the range's Q tiles in pairs.  Per Q tile the
+// arithmetic and the KV visit order are those of attn_fwd_kernel, so the output is the same
+// bit for bit; what goes away is the per-tile copy and barrier and the per-workgroup
+// start-up, which dominate when a Q tile has only a few KV tiles.  QF: Q arrives as 16-bit
+// values and each group quantizes its own 128-row block (quant_q_raw); the block maximum
+// goes through LDS with one workgroup barrier per pair of tiles, which every wave reaches
+// (the loop over pairs is uniform across the workgroup).  No repair path: the launcher uses
+// attn_fwd_kernel for it.
 // ---------------------------------------------------------------------------------------
 template <int D>
 struct AttnResident {
   static constexpr int NKMAX = D == 128 ? 4 : 8;  // KV tiles held in LDS
 };
 
-template <int D, bool HAS_MASK, bool HAS_BIAS, int ODT>
+template <int D, bool HAS_MASK, bool HAS_BIAS, int ODT, bool QF>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8,
                               const uint8_t* __restrict__ v8t, const float* __restrict__ sq,
                               const float* __restrict__ sk, const float* __restrict__ sv,
                               const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias,
                               void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H,
-                              int Sq, int Sk, int nq, int total) {
+                              int Sq, int Sk, int nq, int total, AttnQ16 qa) {
   typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
   constexpr int NKMAX = AttnResident<D>::NKMAX;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NKMAX * T::BUF];
+  // QF: per-wave block maxima, [pair parity][group][wave]; a pair writes the half its
+  // parity selects, and a wave can only come back to that half after the next pair's
+  // barrier, which every wave reaches after reading this pair's maxima
+  __shared__ float qred[QF ? 16 : 1];
+  __shared__ __attribute__((aligned(16))) float svl[D];  // the loaded head's channel scales sv
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
   const int nk = (Sk + 127) / 128;
@@ -834,25 +879,34 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   // The next tile's Q fragments and scale are fetched before the current tile's output
   // stores: loads and stores retire in order, so a load issued after the stores would wait
   // for them to reach memory.
+  // QF: the next tile's 16-bit Q rows instead (zeros past Sq).
   v8i qnext[D / 64];
   float sqnext = 0.0f;
+  uint4 rawnext[QF ? D / 64 : 1][4];
   auto fetch_q = [&](int id) {
     const int bh_ = id / nq, I_ = id - bh_ * nq;
     const int row = I_ * 128 + wq * 32 + (lane & 31);
-    const uint8_t* qp = q8 + ((int64_t)bh_ * nq * 128 + row) * D + 32 * (lane >> 5);
+    if constexpr (QF) {
+      const int b_ = bh_ / H;
+      AttnCtx<D, HAS_MASK, HAS_BIAS, true>::load_q16(qa, b_, bh_ - b_ * H, row, Sq, lane, rawnext);
+    } else {
+      const uint8_t* qp = q8 + ((int64_t)bh_ * nq * 128 + row) * D + 32 * (lane >> 5);
 #pragma unroll
-    for (int hh = 0; hh < D / 64; ++hh) {
-      const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
-      const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
-      qnext[hh] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      for (int hh = 0; hh < D / 64; ++hh) {
+        const v4i lo = *reinterpret_cast<const v4i*>(qp + 64 * hh);
+        const v4i hi = *reinterpret_cast<const v4i*>(qp + 64 * hh + 16);
+        qnext[hh] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+      sqnext = sq[(int64_t)bh_ * nq + I_];
     }
-    sqnext = sq[(int64_t)bh_ * nq + I_];
   };
+  int parity = 0;
   int loaded = -1;
   int p = ta;
   if (p < tb) {
     bool act;
     fetch_q(pair_item(p, act));
+    wait_vm0();  // so the first pair enters the loop with no load in flight, as later ones do
   }
   while (p < tb) {
     const int bh = p / nq;
@@ -868,7 +922,8 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         dc.dma_v(buf + T::KB, j * 128);
         dc.dma_aux(buf + T::KB + T::VB, j * 128, Sk);
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (threadIdx.x < D) svl[threadIdx.x] = sv[(int64_t)bh * D + threadIdx.x];
+      wait_vm0();
       attn_barrier();
       loaded = bh;
     }
@@ -876,15 +931,29 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     const int id = pair_item(p, active);
     AttnCtx<D, HAS_MASK, HAS_BIAS, true> cx(nullptr, k8, v8t, nullptr, sk, key_mask, key_bias, H, Sk, nq, id, wq,
                                             lane);
+    if constexpr (QF) {
+      // every wave, active or not, takes part (the barrier inside); a stand-in item
+      // quantizes a real tile and writes no scale
+      AttnQ16 qx = qa;
+      if (!active) qx.sq_out = nullptr;
+      cx.template quant_q_raw<ODT>(rawnext, cx.qrow < Sq, qx, nq, qred + 8 * parity + 4 * grp);
+      parity ^= 1;
+    } else {
 #pragma unroll
-    for (int hh = 0; hh < D / 64; ++hh) cx.qf[hh] = qnext[hh];
-    cx.sqI = sqnext;
+      for (int hh = 0; hh < D / 64; ++hh) cx.qf[hh] = qnext[hh];
+      cx.sqI = sqnext;
+    }
     const int np = p + 2 < seg_end ? p + 2 : seg_end;  // first tile of the next pair
+    // the next pair's item, or this one again after the range's last pair (fetched, unused)
+    bool nact;
+    const int nid = np < tb ? pair_item(np, nact) : id;
     AttnState<D> st;
     if (active) {
       st.init();
       int j = (int)(((int64_t)cx.I * nk) / nq);
       for (int i = 0; i < nk; ++i) {
+        // q8 / sq of the next item load under the last tile's products
+        if (!QF && i == nk - 1) fetch_q(nid);
         const uint8_t* buf = smem + j * T::BUF;
         const float skj = cx.skh[j];
         const int kv0 = j * 128;
@@ -894,54 +963,61 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
         const float m_new = attn_codes<HAS_BIAS, false>(s, cx.sqI, skj, st.m, -1.0f, pb);
-        if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
+        // O and l are still zero on the first tile: rescaling them changes no bit
+        if (i > 0 && __builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
         st.m = m_new;
         AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         j = j + 1 == nk ? 0 : j + 1;
       }
     }
-    if (np < tb) {
-      bool nact;
-      fetch_q(pair_item(np, nact));
+    // Every path fetches (an inactive group too), so the fetched registers are dead from
+    // their use at the top of the loop to the fetch; QF's 16-bit rows need too many
+    // registers to be in flight during the products.
+    if (QF || !active) fetch_q(nid);
+    // nothing but the stores is then in flight at the top of the loop
+    wait_vm0();
+    if (active && cx.qrow < Sq) {
+      AttnSv<D> svr;
+      svr.load_lds(svl, lane);
+      attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
     }
-    if (active && cx.qrow < Sq)
-      attn_store<D, ODT>(st, sv, cx.bh, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
     p = np;
   }
 }
 
-// Whether the resident-KV kernel may take a launch: MXF8_ATTN_RESIDENT_KV=0 in the
-// environment turns it off (read at every launch, so a process can compare both kernels).
-inline bool attn_resident_enabled() {
-  const char* e = getenv("MXF8_ATTN_RESIDENT_KV");
-  return !(e != nullptr && e[0] == '0');
-}
-
+// kv_mode MXF8_ATTN_KV_AUTO takes attn_fwd_resident_kernel whenever every KV tile of a head
+// fits in LDS and no repair is asked for; MXF8_ATTN_KV_STREAM always takes attn_fwd_kernel.
 template <int D, bool M_, bool B_, bool R_, int ODT>
 static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t, const float* sq, const float* sk,
                         const float* sv, const uint8_t* km, const float* kb, float tau, void* out,
                         const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa,
-                        hipStream_t st) {
+                        int kv_mode, hipStream_t st) {
   const int64_t nq = cdiv(Sq, 128);
   const int64_t nk = cdiv(Sk, 128);
   const int64_t total = nq * B * H;
-  if (!R_ && qa == nullptr && nk <= AttnResident<D>::NKMAX && attn_resident_enabled()) {
+  const AttnQ16 qv = qa != nullptr ? *qa : AttnQ16{nullptr, 0, 0, 0, 0.0f, nullptr};
+  if (!R_ && kv_mode == MXF8_ATTN_KV_AUTO && nk <= AttnResident<D>::NKMAX) {
     const int cus = device_cus();
     const unsigned g = (unsigned)(cus > 0 && total > cus ? cus : total);
-    attn_fwd_resident_kernel<D, M_, B_, ODT><<<dim3(g), 512, 0, st>>>(
-        q8, k8, v8t, sq, sk, sv, km, kb, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
-        (int)total);
+    if (qa != nullptr)
+      attn_fwd_resident_kernel<D, M_, B_, ODT, true><<<dim3(g), 512, 0, st>>>(
+          nullptr, k8, v8t, nullptr, sk, sv, km, kb, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk,
+          (int)nq, (int)total, qv);
+    else
+      attn_fwd_resident_kernel<D, M_, B_, ODT, false><<<dim3(g), 512, 0, st>>>(
+          q8, k8, v8t, sq, sk, sv, km, kb, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
+          (int)total, qv);
     return;
   }
   const dim3 grid((unsigned)(nq * B * H));
   if (qa != nullptr)
     attn_fwd_kernel<D, M_, B_, R_, ODT, true><<<grid, 256, 0, st>>>(
         nullptr, k8, v8t, nullptr, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk,
-        (int)nq, *qa);
+        (int)nq, qv);
   else
     attn_fwd_kernel<D, M_, B_, R_, ODT, false><<<grid, 256, 0, st>>>(
         q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
-        AttnQ16{nullptr, 0, 0, 0, 0.0f, nullptr});
+        qv);
 }
 
 // qa == nullptr: Q from q8 / sq; otherwise the fused Q quantizer reads qa.
@@ -949,11 +1025,12 @@ template <int D, int ODT>
 static void attn_dispatch_flags(bool hm, bool hb, bool rep, const uint8_t* q8, const uint8_t* k8,
                                 const uint8_t* v8t, const float* sq, const float* sk, const float* sv,
                                 const uint8_t* km, const float* kb, float tau, void* out, const int64_t os[4],
-                                int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa, hipStream_t st) {
-#define MXF8_ATTN_CASE(M_, B_, R_)                                                                           \
-  if (hm == M_ && hb == B_ && rep == R_) {                                                                   \
-    launch_attn<D, M_, B_, R_, ODT>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os, B, H, Sq, Sk, qa, st); \
-    return;                                                                                                  \
+                                int64_t B, int64_t H, int64_t Sq, int64_t Sk, const AttnQ16* qa, int kv_mode,
+                                hipStream_t st) {
+#define MXF8_ATTN_CASE(M_, B_, R_)                                                                                \
+  if (hm == M_ && hb == B_ && rep == R_) {                                                                        \
+    launch_attn<D, M_, B_, R_, ODT>(q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os, B, H, Sq, Sk, qa, kv_mode, st); \
+    return;                                                                                                       \
   }
   MXF8_ATTN_CASE(false, false, false)
   MXF8_ATTN_CASE(true, false, false)
@@ -973,7 +1050,7 @@ static void attn_dispatch_flags(bool hm, bool hb, bool rep, const uint8_t* q8, c
                                  const uint8_t* v8t, const float* sq, const float* sk, const float* sv,     \
                                  const uint8_t* km, const float* kb, float tau, void* out,                  \
                                  const int64_t os[4], int64_t B, int64_t H, int64_t Sq, int64_t Sk,         \
-                                 const AttnQ16* qa, hipStream_t st)
+                                 const AttnQ16* qa, int kv_mode, hipStream_t st)
 MXF8_ATTN_DECL(128, 0);
 MXF8_ATTN_DECL(128, 1);
 MXF8_ATTN_DECL(64, 0);

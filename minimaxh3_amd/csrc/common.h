@@ -57,6 +57,29 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)f);
 }
 
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left free) through the builtin: the compiler's
+// own wait insertion takes it into account (it cannot see into inline asm), so it knows
+// that no load is in flight after it and adds no wait of its own for one.  The memory
+// clobber keeps LDS accesses from moving across it.
+__device__ __forceinline__ void wait_vm0() {
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  asm volatile("" ::: "memory");
+}
+
+// Two fp32 values -> two 16-bit values (ODT = MXF8_BF16 / MXF8_F16), a in the low half, in
+// one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: round to nearest even, the same bits as
+// f32_to_bf16_bits / f32_to_f16_bits for every non-NaN input (NaN stays NaN).
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+template <int ODT>
+__device__ __forceinline__ uint32_t cvt_pk_16(float a, float b) {
+  const v2f v = {a, b};
+  if constexpr (ODT == 0)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2bf));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2h));
+}
+
 // Input element loaders: DT = MXF8_BF16 / MXF8_F16 / MXF8_F32.
 template <int DT> struct Elem;
 template <> struct Elem<MXF8_BF16> {

@@ -62,7 +62,6 @@ __device__ __forceinline__ float gelu_tanh_f32(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 // fp32 -> bf16 -> fp32 and fp32 pair -> packed bf16 pair, both with the hardware
 // round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
@@ -231,7 +230,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     gemm_dma<C>(rsrc_s(lora_b, tn_ * C::BN, N, C::BN, lrow), rsrc_s(lora_t, tm_ * C::BM, M, C::BM, lrow), dst,
                 lane_off_l, lrow, wave, c * GEMM_BK);
   };
-  static_assert(C::THREADS >= C::BM + C::BN, "one thread per epilogue operand");
+  static_assert(C::THREADS == C::BM + C::BN, "one thread per epilogue operand");
 
   int s = blockIdx.x;
   int tm, tn;
@@ -243,18 +242,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
   for (; s < ntiles; s += gridDim.x) {
     const int m0 = tm * C::BM, n0 = tn * C::BN;
     // the tile's channel scales, bias and token scales, read now (their latency hides
-    // behind the mainloop) and handed to the epilogue through LDS after it
-    float ep_v0 = 0.0f, ep_v1 = 0.0f;
-    if ((int)threadIdx.x < C::BN) {
-      const int n = n0 + threadIdx.x;
-      if (n < N) {
-        ep_v0 = sw[n];
-        if (bias) ep_v1 = bf16_bits_to_f32(bias[n]);
-      }
-    } else if ((int)threadIdx.x < C::BN + C::BM) {
-      const int m = m0 + threadIdx.x - C::BN;
-      if (m < M) ep_v0 = sa[m];
-    }
+    // behind the mainloop) and handed to the epilogue through LDS after it.  Thread t < BN
+    // reads channel n0 + t, the next BM threads token m0 + t - BN; indices past the end read
+    // the last element and are zeroed at the hand-over.  Nothing here waits for a load: a
+    // wait issued now would also wait for the previous tile's output stores.
+    // (Unconditional loads from valid addresses, selected when handed over: a load under a
+    // condition makes the compiler wait for it at the end of the condition.)
+    const bool ep_chan = (int)threadIdx.x < C::BN;
+    const int ep_idx = ep_chan ? n0 + (int)threadIdx.x : m0 + (int)threadIdx.x - C::BN;
+    const bool ep_ok = ep_idx < (ep_chan ? N : M);
+    const float ep_v0 = *(ep_chan ? sw + min(ep_idx, N - 1) : sa + min(ep_idx, M - 1));
+    const bool ep_hb = ep_chan && bias != nullptr;
+    const uint16_t ep_bias = *(ep_hb ? bias + min(ep_idx, N - 1) : reinterpret_cast<const uint16_t*>(sw));
     // the next tile of this workgroup, whose first stage is copied during this epilogue
     const int s_next = s + gridDim.x;
     int tm_n = 0, tn_n = 0;
@@ -268,13 +267,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
-    for (int ks = 0; ks < nk; ++ks, ++gs) {
+    // nk >= 1 (K >= 16): a do-while tells the compiler that the wait below runs before the
+    // epilogue, which then waits for none of the loads issued before the mainloop (a wait
+    // there would also wait for the next tile's first stage, in flight by then).
+    int ks = 0;
+    do {
       uint8_t* cur = smem + (gs & 1) * C::STAGE;
       uint8_t* nxt = smem + ((gs + 1) & 1) * C::STAGE;
       // Stage gs is this wave's only DMA in flight (and the epilogue operands, older).
       // After the barrier every wave's copy of it has landed and every wave has finished
       // stage gs-1, whose buffer then takes stage gs+1 while stage gs is multiplied.
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      wait_vm0();
       block_barrier();
       if (KTAIL && ks == nk - 1) {
         zero_tail<C>(cur, (K % GEMM_BK) >> 4);
@@ -290,7 +293,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, 0);
       }
       mma_stage<C>(cur, wrow0, xrow0, lane, acc);
-    }
+      ++gs;
+    } while (++ks < nk);
 
     // ---- LoRA chunks (LDS mode) ---------------------------------------------------------
     // chunk 0 is in buffer gs & 1; the last K stage's buffer (gs + 1) & 1 is free once
@@ -298,13 +302,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     uint8_t* const lch0 = smem + (gs & 1) * C::STAGE;
     uint8_t* const lch1 = smem + ((gs + 1) & 1) * C::STAGE;
     if constexpr (LM == LORA_LDS) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      wait_vm0();
       block_barrier();
       if (nl == 2) {
         // second chunk (r > 64): its copy is exposed; the next tile's first stage waits
         // for the end of the epilogue
         lora_dma(lch1, tm, tn, 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_vm0();
         block_barrier();
       } else if (s_next < ntiles) {
         wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
@@ -321,11 +325,11 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     // ---- epilogue ----------------------------------------------------------------------
     // (the previous tile's epilogue reads of these LDS words finished before the barrier
     // at the top of this tile's last stage)
-    if ((int)threadIdx.x < C::BN) {
-      ep_sw[threadIdx.x] = ep_v0;
-      ep_b[threadIdx.x] = ep_v1;
-    } else if ((int)threadIdx.x < C::BN + C::BM) {
-      ep_sa[threadIdx.x - C::BN] = ep_v0;
+    if (ep_chan) {
+      ep_sw[threadIdx.x] = ep_ok ? ep_v0 : 0.0f;
+      ep_b[threadIdx.x] = ep_ok && ep_hb ? bf16_bits_to_f32(ep_bias) : 0.0f;
+    } else {
+      ep_sa[threadIdx.x - C::BN] = ep_ok ? ep_v0 : 0.0f;
     }
     block_barrier();
 
@@ -518,7 +522,7 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restric
     uint8_t* cur = smem + (ks & 1) * STAGE;
     // stage ks is this wave's only DMA in flight; after the barrier every wave's copy of
     // it has landed and every wave has finished stage ks - 1, whose buffer takes ks + 1
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vm0();
     block_barrier();
     if (ks == nk - 1 && (K & 63)) {
       // zero the chunks at or past K (they hold the next row's elements)

@@ -324,11 +324,13 @@ def _(k, v):
 @torch.library.custom_op("mxf8::attn_fwd", mutates_args=())
 def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Tensor, sk: torch.Tensor,
              sv: torch.Tensor, key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, repair_tau: float,
-             like: torch.Tensor, Sk: int) -> torch.Tensor:
+             like: torch.Tensor, Sk: int, kv_mode: int = 0) -> torch.Tensor:
     """FP8 flash-attention forward (fp8_attention.py:185-297).
 
     ``like`` is the original query: the output has its shape, dtype and strides (the
-    kernel writes through the strides, so permuted query layouts stay correct).
+    kernel writes through the strides, so permuted query layouts stay correct).  kv_mode
+    0 holds a head's K/V in LDS when they fit (Sk <= 512 at D = 128, no repair), 1 always
+    streams K/V tiles; both give the same bits.
     """
     _prep(q8, "attn_fwd")
     B, H, Sq, D = like.shape
@@ -338,12 +340,12 @@ def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Te
         N.check(N.load().mxf8_attn_fwd(
             q8.data_ptr(), k8.data_ptr(), v8t.data_ptr(), sq.data_ptr(), sk.data_ptr(), sv.data_ptr(),
             N.ptr(km), N.ptr(kb), float(repair_tau), out.data_ptr(), N.dtype_code(out.dtype), N.strides4(out),
-            B, H, Sq, Sk, D, N.stream_of(q8)), "attn_fwd")
+            B, H, Sq, Sk, D, int(kv_mode), N.stream_of(q8)), "attn_fwd")
     return out
 
 
 @attn_fwd.register_fake
-def _(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, like, Sk):
+def _(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, like, Sk, kv_mode=0):
     return torch.empty_like(like)
 
 
@@ -359,9 +361,10 @@ def attn_fwd_q_supported(q: torch.Tensor) -> bool:
 @torch.library.custom_op("mxf8::attn_fwd_q", mutates_args=())
 def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, sk: torch.Tensor, sv: torch.Tensor,
                key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, repair_tau: float,
-               Sk: int) -> torch.Tensor:
+               Sk: int, kv_mode: int = 0) -> torch.Tensor:
     """attn_quant_q + attn_fwd in one launch (fp8_attention.py:321-336 and 380-402): each
-    workgroup quantizes its own 128-row Q block; same output bit for bit."""
+    128-row Q block is quantized inside the launch; same output bit for bit.  kv_mode as
+    attn_fwd."""
     _prep(q, "attn_fwd_q")
     if not attn_fwd_q_supported(q):
         raise ValueError("attn_fwd_q: q must be bf16/fp16 with unit channel stride, other strides multiples of 8 "
@@ -369,7 +372,7 @@ def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, s
     if q.data_ptr() % 16:
         # a view that starts off a 16-byte boundary: the two launches give the same bits
         q8, sq = attn_quant_q(q, c)
-        return attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, q, Sk)
+        return attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, q, Sk, kv_mode)
     B, H, Sq, D = q.shape
     out = torch.empty_like(q)
     km, kb = key_operands(key_mask, key_bias, B, Sk, q.device)
@@ -377,12 +380,12 @@ def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, s
         N.check(N.load().mxf8_attn_fwd_q(
             q.data_ptr(), N.strides4(q), float(c), k8.data_ptr(), v8t.data_ptr(), sk.data_ptr(), sv.data_ptr(),
             N.ptr(km), N.ptr(kb), float(repair_tau), None, out.data_ptr(), N.dtype_code(out.dtype), N.strides4(out),
-            B, H, Sq, Sk, D, N.stream_of(q)), "attn_fwd_q")
+            B, H, Sq, Sk, D, int(kv_mode), N.stream_of(q)), "attn_fwd_q")
     return out
 
 
 @attn_fwd_q.register_fake
-def _(q, c, k8, v8t, sk, sv, key_mask, key_bias, repair_tau, Sk):
+def _(q, c, k8, v8t, sk, sv, key_mask, key_bias, repair_tau, Sk, kv_mode=0):
     return torch.empty_like(q)
 
 

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(N.lib_path())
     for name in _declared():
         assert hasattr(raw, name), name
-    assert lib.mxf8_abi_version() == 100
+    assert lib.mxf8_abi_version() == 200
     assert lib.mxf8_last_error() is not None
 
 
@@ -89,21 +89,23 @@ def test_attention_argument_checks(lib):
     assert lib.mxf8_attn_quant_q(d, 0, st, 1, 1, 16, 96, 1.0, d, d, None) == 1 and "D must be" in _err(lib)
     assert lib.mxf8_attn_quant_q(d, 2, st, 1, 1, 16, 128, 1.0, d, d, None) == 1 and "dtype" in _err(lib)
     assert lib.mxf8_attn_kmean(d, 0, st, 1, 1, 16, 128, d, None, None) == 1
-    assert lib.mxf8_attn_fwd(d, d, d, d, d, d, None, None, -1.0, d, 0, st, 1, 1, 0, 16, 128, None) == 1
-    assert lib.mxf8_attn_fwd(d, d, d, d, d, d, None, None, -1.0, d, 2, st, 1, 1, 8, 16, 128, None) == 1
+    assert lib.mxf8_attn_fwd(d, d, d, d, d, d, None, None, -1.0, d, 0, st, 1, 1, 0, 16, 128, 0, None) == 1
+    assert lib.mxf8_attn_fwd(d, d, d, d, d, d, None, None, -1.0, d, 2, st, 1, 1, 8, 16, 128, 0, None) == 1
+    assert lib.mxf8_attn_fwd(d, d, d, d, d, d, None, None, -1.0, d, 0, st, 1, 1, 8, 16, 128, 2, None) == 1 \
+        and "kv_mode" in _err(lib)
     qs = N._I64x4(128 * 16, 128 * 16, 128, 1)
     assert lib.mxf8_attn_fwd_q(None, qs, 1.0, d, d, d, d, None, None, -1.0, None, d, 0, st, 1, 1, 16, 16, 128,
-                               None) == 1 and "null" in _err(lib)
+                               0, None) == 1 and "null" in _err(lib)
     bad = N._I64x4(128 * 16, 128 * 16, 128, 2)  # channel stride 2
     assert lib.mxf8_attn_fwd_q(d, bad, 1.0, d, d, d, d, None, None, -1.0, None, d, 0, st, 1, 1, 16, 16, 128,
-                               None) == 1 and "unit channel stride" in _err(lib)
+                               0, None) == 1 and "unit channel stride" in _err(lib)
     odd = N._I64x4(128 * 16, 128 * 16, 132, 1)  # row stride not a multiple of 8
     assert lib.mxf8_attn_fwd_q(d, odd, 1.0, d, d, d, d, None, None, -1.0, None, d, 0, st, 1, 1, 16, 16, 128,
-                               None) == 1 and "multiples of 8" in _err(lib)
+                               0, None) == 1 and "multiples of 8" in _err(lib)
     assert lib.mxf8_attn_fwd_q(ctypes.c_void_p(264), qs, 1.0, d, d, d, d, None, None, -1.0, None, d, 0, st, 1, 1,
-                               16, 16, 128, None) == 1 and "alignment" in _err(lib)
+                               16, 16, 128, 0, None) == 1 and "alignment" in _err(lib)
     assert lib.mxf8_attn_fwd_q(d, qs, 1.0, d, d, d, d, None, None, -1.0, None, d, 0, st, 1, 1, 16, 16, 96,
-                               None) == 1 and "D must be" in _err(lib)
+                               0, None) == 1 and "D must be" in _err(lib)
     assert lib.mxf8_attn_workspace_bytes(1, 24, 20280, 20280, 128) > 0
     assert lib.mxf8_attn_workspace_bytes(0, 24, 20280, 20280, 128) == 0
     # K and V together: shape, dtype and pointer checks run before any launch

@@ -40,7 +40,7 @@ def _bits(t):
     return t.view(torch.int16).cpu()
 
 
-def _fused_abi(q, c, k8, v8t, sk, sv, km, kb, tau, Sk, nq):
+def _fused_abi(q, c, k8, v8t, sk, sv, km, kb, tau, Sk, nq, kv_mode):
     """mxf8_attn_fwd_q through the C ABI, with the Q scales written out."""
     from minimaxh3_amd import _native as N
     B, H, Sq, D = q.shape
@@ -50,7 +50,7 @@ def _fused_abi(q, c, k8, v8t, sk, sv, km, kb, tau, Sk, nq):
     N.check(N.load().mxf8_attn_fwd_q(
         q.data_ptr(), N.strides4(q), float(c), k8.data_ptr(), v8t.data_ptr(), sk.data_ptr(), sv.data_ptr(),
         N.ptr(km), N.ptr(kb), float(tau), sq.data_ptr(), out.data_ptr(), N.dtype_code(out.dtype), N.strides4(out),
-        B, H, Sq, Sk, D, N.stream_of(q)), "attn_fwd_q")
+        B, H, Sq, Sk, D, kv_mode, N.stream_of(q)), "attn_fwd_q")
     torch.cuda.synchronize()
     return out, sq
 
@@ -97,10 +97,12 @@ def test_fused_q_equals_two_calls_and_oracle(B, H, Sq, Sk, D, dtype, layout, use
     q8, sq = ops.attn_quant_q(qg, float(c))
     two = ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, float(tau), qg, Sk)
     nq = -(-Sq // 128)
-    fused, sq_f = _fused_abi(qg, c, k8, v8t, sk, sv, km, kb, tau, Sk, nq)
-    assert fused.stride() == two.stride()
-    assert torch.equal(_bits(fused), _bits(two))
-    assert torch.equal(sq_f, sq)
+    # kv_mode 0 takes the resident-K/V kernel where K/V fit in LDS and tau < 0, 1 streams
+    for kv_mode in (0, 1):
+        fused, sq_f = _fused_abi(qg, c, k8, v8t, sk, sv, km, kb, tau, Sk, nq, kv_mode)
+        assert fused.stride() == two.stride()
+        assert torch.equal(_bits(fused), _bits(two)), kv_mode
+        assert torch.equal(sq_f, sq), kv_mode
     np.testing.assert_array_equal(sq_f.cpu().numpy(), oa.quantize_q(q, c)[1])
     via_op = ops.attn_fwd_q(qg, float(c), k8, v8t, sk, sv, km, kb, float(tau), Sk)
     assert torch.equal(_bits(via_op), _bits(fused))

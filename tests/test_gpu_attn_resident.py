@@ -1,14 +1,14 @@
 """GPU parity of the resident-KV attention kernel (short key sequences).
 
-When every KV tile of a head fits in LDS (Sk <= 512 at D = 128, <= 1024 at D = 64), Q comes
-from q8 / sq (mxf8_attn_fwd) and no repair is asked for, the launcher runs
-attn_fwd_resident_kernel.  Per Q tile it performs
+When every KV tile of a head fits in LDS (Sk <= 512 at D = 128, <= 1024 at D = 64) and no
+repair is asked for, the launcher runs attn_fwd_resident_kernel.  Per Q tile it performs
 attn_fwd_kernel's arithmetic in the same KV visit order, so both kernels must give the same
-bits; MXF8_ATTN_RESIDENT_KV=0 selects attn_fwd_kernel for the comparison.  The output is
-also held to the attention bar against the oracle.
+bits; kv_mode 1 (MXF8_ATTN_KV_STREAM) selects attn_fwd_kernel for the comparison.  With Q
+as 16-bit values (mxf8_attn_fwd_q) each group quantizes its own Q block inside the resident
+kernel, and the result must equal the two-call path's.  The output is also held to the
+attention bar against the oracle.
 """
 import math
-import os
 import sys
 
 import numpy as np
@@ -27,18 +27,9 @@ def _say(msg):
 
 
 def _both(fn):
-    """fn() with the resident kernel allowed, then with it switched off."""
-    saved = os.environ.get("MXF8_ATTN_RESIDENT_KV")
-    try:
-        os.environ.pop("MXF8_ATTN_RESIDENT_KV", None)
-        a = fn()
-        os.environ["MXF8_ATTN_RESIDENT_KV"] = "0"
-        b = fn()
-    finally:
-        if saved is None:
-            os.environ.pop("MXF8_ATTN_RESIDENT_KV", None)
-        else:
-            os.environ["MXF8_ATTN_RESIDENT_KV"] = saved
+    """fn(kv_mode) with the resident kernel allowed (0), then with K/V streamed (1)."""
+    a = fn(0)
+    b = fn(1)
     torch.cuda.synchronize()
     return a, b
 
@@ -81,16 +72,20 @@ def test_resident_kv_equals_streaming_kernel(B, H, Sq, Sk, D, dtype, use_mask, u
     k8, sk = ops.attn_quant_k(kg, ops.attn_kmean(kg))
     v8t, sv = ops.attn_quant_v(vg)
     q8, sq = ops.attn_quant_q(qg, float(c))
-    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, qg, Sk))
+    res, stream = _both(lambda m: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, qg, Sk, m))
     assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    fres, fstream = _both(lambda m: ops.attn_fwd_q(qg, float(c), k8, v8t, sk, sv, km, kb, -1.0, Sk, m))
+    assert torch.equal(fres.view(torch.int16), res.view(torch.int16))
+    assert torch.equal(fstream.view(torch.int16), res.view(torch.int16))
     ref, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=-1.0,
                               out_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
     assert_attn_close(res.float().cpu().numpy(), ref)
 
 
 def test_resident_kv_text_cross_attention_full_size():
-    """The joint workload's text cross-attention (B=2, H=24, Sq=21304, Sk=512): both kernels
-    give the same bits at full size."""
+    """The joint workload's text cross-attention (B=2, H=24, Sq=21304, Sk=512): both kernels,
+    with Q from q8 / sq and with Q quantized inside the launch, give the same bits at full
+    size."""
     _say("attn resident-KV full-size cross-attention")
     from minimaxh3_amd import ops
     B, H, Sq, Sk, D = 2, 24, 21304, 512, 128
@@ -102,8 +97,11 @@ def test_resident_kv_text_cross_attention_full_size():
     k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
     v8t, sv = ops.attn_quant_v(v)
     q8, sq = ops.attn_quant_q(q, c)
-    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, Sk))
+    res, stream = _both(lambda m: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, Sk, m))
     assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    fres, fstream = _both(lambda m: ops.attn_fwd_q(q, c, k8, v8t, sk, sv, None, None, -1.0, Sk, m))
+    assert torch.equal(fres.view(torch.int16), res.view(torch.int16))
+    assert torch.equal(fstream.view(torch.int16), res.view(torch.int16))
     assert torch.isfinite(res.float()).all()
 
 
@@ -127,6 +125,9 @@ def test_resident_kv_many_tiles_per_workgroup_mask_bias(D, Sk):
     k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
     v8t, sv = ops.attn_quant_v(v)
     q8, sq = ops.attn_quant_q(q, c)
-    res, stream = _both(lambda: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, q, Sk))
+    res, stream = _both(lambda m: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, kb, -1.0, q, Sk, m))
     assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    fres, fstream = _both(lambda m: ops.attn_fwd_q(q, c, k8, v8t, sk, sv, km, kb, -1.0, Sk, m))
+    assert torch.equal(fres.view(torch.int16), res.view(torch.int16))
+    assert torch.equal(fstream.view(torch.int16), res.view(torch.int16))
     assert torch.isfinite(res.float()).all()

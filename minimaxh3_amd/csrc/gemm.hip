@@ -178,6 +178,11 @@ __device__ __forceinline__ void lora_chunk_mma(const uint8_t* chunk, int wrow, i
   }
 }
 
+// Registers 4 q .. 4 q + 3 of an accumulator block.
+__device__ __forceinline__ v4f quad4(const v16f& c, int q) {
+  return v4f{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
+}
+
 // LM (LoRA mode): with lora_t [M, r] = bf16(x A^T) and lora_b [N, r] = B, the epilogue adds
 // the reference's LoRA branch bf16(bf16(t B^T) * lora_scale) to the bf16 linear output.
 // In LORA_LDS mode the t and B tiles (r <= 128: one or two 64-column chunks) are copied
@@ -192,8 +197,10 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     int K, int64_t ld_out, int tiles_m, int tiles_n, int group_m) {
   constexpr int TM = C::TM, TN = C::TN;
   constexpr int EP_BYTES = (2 * C::BN + C::BM) * 4;  // channel scales, bias (fp32), token scales
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + EP_BYTES];
-  static_assert(2 * C::STAGE + EP_BYTES <= 160 * 1024, "LDS exceeds the 160 KB of a CU");
+  // with LoRA chunks in LDS: each wave's 2 KB output staging region (one 32 x 32 block)
+  constexpr int LS_BYTES = LM == LORA_LDS ? C::NW * 2048 : 0;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE + EP_BYTES + LS_BYTES];
+  static_assert(2 * C::STAGE + EP_BYTES + LS_BYTES <= 160 * 1024, "LDS exceeds the 160 KB of a CU");
   float* const ep_sw = reinterpret_cast<float*>(smem + 2 * C::STAGE);  // [BN]
   float* const ep_b = ep_sw + C::BN;                                   // [BN]
   float* const ep_sa = ep_b + C::BN;                                   // [BM]
@@ -335,12 +342,51 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 
     // acc[a][b] register i: channel n = nb + 8 (i/4) + 4 g + i%4, token m = mb + lane%32.
     const int g = lane >> 5;
-    const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)out) & 7) == 0);
-    bool staged = false;
-    if constexpr (LM == LORA_NONE) {
-      staged = ((ld_out & 7) == 0) && ((((uintptr_t)out) & 15) == 0) && (m0 + C::BM <= M) && (n0 + C::BN <= N);
-    }
-    if (staged) {
+    // The LoRA branch of block (a, b) (zero without LoRA).
+    auto lora_block = [&](int a, int b) {
+      v16f lacc;
+      if constexpr (LM != LORA_NONE) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+      }
+      const int nl_ = wrow0 + 32 * a, ml = xrow0 + 32 * b + (lane & 31);
+      if constexpr (LM == LORA_LDS) {
+        lora_chunk_mma<C>(lch0, nl_ + (lane & 31), ml, g, lacc);
+        if (nl == 2) lora_chunk_mma<C>(lch1, nl_ + (lane & 31), ml, g, lacc);
+      } else if constexpr (LM == LORA_GLOBAL) {
+        // LoRA up-projection on the bf16 MFMA from global memory (r > 128)
+        const uint16_t* brow = lora_b + (int64_t)min(n0 + nl_ + (lane & 31), N - 1) * lora_r + 8 * g;
+        const uint16_t* trow = lora_t + (int64_t)min(m0 + ml, M - 1) * lora_r + 8 * g;
+        for (int kk = 0; kk < lora_r; kk += 16) {
+          const v8bf bo = *reinterpret_cast<const v8bf*>(brow + kk);
+          const v8bf to = *reinterpret_cast<const v8bf*>(trow + kk);
+          lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bo, to, lacc, 0, 0, 0);
+        }
+      }
+      return lacc;
+    };
+    // Output values of accumulators x (registers 4 q .. 4 q + 3 of a block, whose LoRA
+    // branch is lacc), packed as two bf16 pairs.
+    auto out_quad = [&](const v4f x, int q, const v16f& lacc, float sam, const v4f& swq, const v4f& bq) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = __builtin_fmaf(x[e] * sam, swq[e], bq[e]);
+        // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch * scale,
+        // bf16 sum; GELU-tanh acts on the bf16 result
+        if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
+        if constexpr (LM != LORA_NONE) {
+          const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
+          v[e] = bf16r(v[e] + br);
+        }
+        if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(v[e]);
+      }
+      return make_uint2(bf16x2(v[0], v[1]), bf16x2(v[2], v[3]));
+    };
+
+    const bool staged =
+        ((ld_out & 7) == 0) && ((((uintptr_t)out) & 15) == 0) && (m0 + C::BM <= M) && (n0 + C::BN <= N);
+    if (staged && LM != LORA_LDS) {
       // Whole tile in range: each 32-token round of this wave goes through a private 8 KB
       // LDS region in the buffer of the last K stage (free after the barrier above; the
       // next tile's first copy into it waits for the barrier at the top of its first
@@ -356,21 +402,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         const float sam = ep_sa[xrow0 + 32 * b + r];
 #pragma unroll
         for (int a = 0; a < TN; ++a) {
+          const v16f lacc = lora_block(a, b);
           const int nl_ = wrow0 + 32 * a;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const v4f swq = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
-            const v4f bq = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = __builtin_fmaf(acc[a][b][4 * q + e] * sam, swq[e], bq[e]);
-              if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(bf16r(v[e]));
-            }
-            const int chunk = 4 * a + q;
-            *reinterpret_cast<uint2*>(wreg + r * RB + ((chunk ^ (r & (NCH - 1))) << 4) + 8 * g) =
-                make_uint2(bf16x2(v[0], v[1]), bf16x2(v[2], v[3]));
-          }
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(wreg + r * RB + (((4 * a + q) ^ (r & (NCH - 1))) << 4) + 8 * g) =
+                out_quad(quad4(acc[a][b], q), q, lacc, sam, *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g),
+                         *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -381,66 +419,70 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
-    }
+    } else if (staged) {
+      // LoRA chunks and the next tile's first stage fill both stage buffers: each 32 x 32
+      // block goes through a private 2 KB region of its own and leaves as 16-byte stores
+      // covering 64-byte row segments.
+      uint8_t* const wreg = smem + 2 * C::STAGE + EP_BYTES + wave * 2048;
+      const int r = lane & 31;
 #pragma unroll
-    for (int a = 0; a < TN && !staged; ++a) {
-      const int nl_ = wrow0 + 32 * a;  // tile-local channel base
-      const int nb = n0 + nl_;
-      v4f swq[4], bq[4];
+      for (int a = 0; a < TN; ++a) {
+        const int nl_ = wrow0 + 32 * a;
+        v4f swq[4], bq[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
-        bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
-      }
-#pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        const int ml = xrow0 + 32 * b + (lane & 31);
-        const int m = m0 + ml;
-        const float sam = ep_sa[ml];
-        v16f lacc;
-        if constexpr (LM != LORA_NONE) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) lacc[i] = 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
+          bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
         }
-        if constexpr (LM == LORA_LDS) {
-          lora_chunk_mma<C>(lch0, nl_ + (lane & 31), ml, g, lacc);
-          if (nl == 2) lora_chunk_mma<C>(lch1, nl_ + (lane & 31), ml, g, lacc);
-        } else if constexpr (LM == LORA_GLOBAL) {
-          // LoRA up-projection on the bf16 MFMA from global memory (r > 128)
-          const uint16_t* brow = lora_b + (int64_t)min(nb + (lane & 31), N - 1) * lora_r + 8 * g;
-          const uint16_t* trow = lora_t + (int64_t)min(m, M - 1) * lora_r + 8 * g;
-          for (int kk = 0; kk < lora_r; kk += 16) {
-            const v8bf bo = *reinterpret_cast<const v8bf*>(brow + kk);
-            const v8bf to = *reinterpret_cast<const v8bf*>(trow + kk);
-            lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bo, to, lacc, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const v16f lacc = lora_block(a, b);
+          const float sam = ep_sa[xrow0 + 32 * b + r];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(wreg + r * 64 + ((q ^ (r & 3)) << 4) + 8 * g) =
+                out_quad(quad4(acc[a][b], q), q, lacc, sam, swq[q], bq[q]);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int row = 16 * i + lane / 4, ch = lane % 4;
+            const uint4 val = *reinterpret_cast<const uint4*>(wreg + row * 64 + ((ch ^ (row & 3)) << 4));
+            *reinterpret_cast<uint4*>(out + (int64_t)(m0 + xrow0 + 32 * b + row) * ld_out + n0 + nl_ + ch * 8) = val;
           }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
-        if (m < M) {
+      }
+    } else {
+      const bool vec_ok = ((N & 3) == 0) && ((ld_out & 3) == 0) && ((((uintptr_t)out) & 7) == 0);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int n = nb + 8 * q + 4 * g;
-            float v[4];
+      for (int a = 0; a < TN; ++a) {
+        const int nl_ = wrow0 + 32 * a;  // tile-local channel base
+        v4f swq[4], bq[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = __builtin_fmaf(acc[a][b][4 * q + e] * sam, swq[q][e], bq[q][e]);
-              // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch *
-              // scale, bf16 sum; GELU-tanh acts on the bf16 result
-              if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
-              if constexpr (LM != LORA_NONE) {
-                const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
-                v[e] = bf16r(v[e] + br);
+        for (int q = 0; q < 4; ++q) {
+          swq[q] = *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g);
+          bq[q] = *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g);
+        }
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const int ml = xrow0 + 32 * b + (lane & 31);
+          const int m = m0 + ml;
+          const v16f lacc = lora_block(a, b);
+          if (m < M) {
+            const float sam = ep_sa[ml];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int n = n0 + nl_ + 8 * q + 4 * g;
+              const uint2 o = out_quad(quad4(acc[a][b], q), q, lacc, sam, swq[q], bq[q]);
+              uint16_t* dst = out + (int64_t)m * ld_out + n;
+              if (vec_ok && n + 3 < N) {
+                *reinterpret_cast<uint2*>(dst) = o;
+              } else {
+                const uint16_t oo[4] = {(uint16_t)o.x, (uint16_t)(o.x >> 16), (uint16_t)o.y, (uint16_t)(o.y >> 16)};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < N) dst[e] = oo[e];
               }
-              if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(v[e]);
-            }
-            const uint32_t o01 = bf16x2(v[0], v[1]), o23 = bf16x2(v[2], v[3]);
-            uint16_t* dst = out + (int64_t)m * ld_out + n;
-            if (vec_ok && n + 3 < N) {
-              *reinterpret_cast<uint2*>(dst) = make_uint2(o01, o23);
-            } else {
-              const uint16_t o[4] = {(uint16_t)o01, (uint16_t)(o01 >> 16), (uint16_t)o23, (uint16_t)(o23 >> 16)};
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (n + e < N) dst[e] = o[e];
             }
           }
         }

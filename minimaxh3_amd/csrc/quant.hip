@@ -10,6 +10,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "rowq.h"
 
 namespace mxf8 {
 
@@ -157,8 +158,6 @@ static int quant_rows_dispatch(const void* x, int64_t M, int64_t K, int64_t ldx,
 //                  n -> bf16, (1 + scale) -> bf16, product -> bf16, sum -> bf16
 // One wave per row with the row in registers (NC 16-byte chunks per lane).
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float bf16_rne(float f) { return (float)(__bf16)f; }
-
 template <int NC, bool EAGER, bool WRITE_Y>
 __global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t C,
                                                                int64_t ldx, int64_t S,
@@ -170,91 +169,21 @@ __global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* _
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
   const int64_t b = row / S;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
-  const uint4* shr = reinterpret_cast<const uint4*>(shift + b * ldm);
-  const uint4* scr = reinterpret_cast<const uint4*>(scale + b * ldm);
   const int64_t nchunk = C / 8;
   uint4 v[NC];
+  row_load_bf16<NC>(x + row * ldx, nchunk, lane, v);
+  float amax = adaln_modulate_bf16<NC, EAGER>(v, C, nchunk, lane, reinterpret_cast<const uint4*>(shift + b * ldm),
+                                               reinterpret_cast<const uint4*>(scale + b * ldm), eps);
+  if constexpr (WRITE_Y) {
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
-  }
-  float sum = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sum += Elem<MXF8_BF16>::lo(w[i]) + Elem<MXF8_BF16>::hi(w[i]);
-  }
-  const float mean = __fdiv_rn(wave_sum(sum), (float)C);
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    if (idx < nchunk) {
-      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float d0 = Elem<MXF8_BF16>::lo(w[i]) - mean, d1 = Elem<MXF8_BF16>::hi(w[i]) - mean;
-        ss = __builtin_fmaf(d0, d0, ss);
-        ss = __builtin_fmaf(d1, d1, ss);
-      }
-    }
-  }
-  const float var = __fdiv_rn(wave_sum(ss), (float)C);
-  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
-  // modulate; y kept as packed bf16 in v
-  float amax = 0.0f;
-  uint16_t* yrow = WRITE_Y ? y + row * C : nullptr;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    if (idx < nchunk) {
-      const uint4 sh = shr[idx], sc = scr[idx];
-      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-      const uint32_t hw[4] = {sh.x, sh.y, sh.z, sh.w}, cw[4] = {sc.x, sc.y, sc.z, sc.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float yy[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float xf = h ? Elem<MXF8_BF16>::hi(w[i]) : Elem<MXF8_BF16>::lo(w[i]);
-          const float shf = h ? Elem<MXF8_BF16>::hi(hw[i]) : Elem<MXF8_BF16>::lo(hw[i]);
-          const float scf = h ? Elem<MXF8_BF16>::hi(cw[i]) : Elem<MXF8_BF16>::lo(cw[i]);
-          const float n = (xf - mean) * rstd;
-          if constexpr (EAGER)
-            yy[h] = bf16_rne(bf16_rne(bf16_rne(n) * bf16_rne(1.0f + scf)) + shf);
-          else
-            yy[h] = bf16_rne(n * (1.0f + scf) + shf);
-          amax = fmaxf(amax, fabsf(yy[h]));
-        }
-        o[i] = (__float_as_uint(yy[0]) >> 16) | (__float_as_uint(yy[1]) & 0xffff0000u);
-      }
-      v[c] = make_uint4(o[0], o[1], o[2], o[3]);
-      if constexpr (WRITE_Y) reinterpret_cast<uint4*>(yrow)[idx] = v[c];
+    for (int c = 0; c < NC; ++c) {
+      const int64_t idx = (int64_t)c * 64 + lane;
+      if (idx < nchunk) reinterpret_cast<uint4*>(y + row * C)[idx] = v[c];
     }
   }
   amax = wave_max(amax);
   const float s = e4m3_scale(amax);
-  const float r = __fdiv_rn(1.0f, s);
-  uint8_t* orow = x8 + row * C;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    if (idx < nchunk) {
-      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-      float f[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[2 * i] = clamp448(div_by_scale(Elem<MXF8_BF16>::lo(w[i]), s, r));
-        f[2 * i + 1] = clamp448(div_by_scale(Elem<MXF8_BF16>::hi(w[i]), s, r));
-      }
-      *reinterpret_cast<uint2*>(orow + idx * 8) = make_uint2(cvt4_e4m3(f[0], f[1], f[2], f[3]),
-                                                             cvt4_e4m3(f[4], f[5], f[6], f[7]));
-    }
-  }
+  row_store_codes_bf16<NC>(v, nchunk, lane, s, __fdiv_rn(1.0f, s), x8 + row * C);
   if (lane == 0) sa[row] = s;
 }
 

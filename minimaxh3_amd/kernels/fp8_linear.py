@@ -132,8 +132,8 @@ class FP8Linear(nn.Module):
         mod.register_buffer("bias", None if bias is None else bias.to(dev, torch.bfloat16).reshape(N).contiguous())
         return mod
 
-    def _lora_operands(self, x2d: torch.Tensor):
-        """(t = bf16(x A^T), B, scale) for the fused epilogue, or (None, None, 0.0).
+    def _lora_ab(self):
+        """(A, B, scale) of the fused epilogue, or None without adapters.
 
         One adapter is applied with exactly the reference's roundings.  Several adapters
         are concatenated along the rank with each scale folded into its B (bf16), which
@@ -142,15 +142,13 @@ class FP8Linear(nn.Module):
         """
         adapters = self.adapters
         if not adapters:
-            return None, None, 0.0
-        xb = x2d if x2d.dtype == torch.bfloat16 else x2d.to(torch.bfloat16)
+            return None
         if torch.compiler.is_compiling():
             # Traced (the reference compiles each block before LoRAs are appended,
             # runtime/model_manager.py:127-141 and runtime/lora.py:263-302): the operands are
             # built in the graph, which for one rank-aligned bf16 adapter is A and B as they
             # stand; the compiler's guards on the adapter list replace the cache below.
-            a, b, scale = self._combine(adapters)
-            return ops.lora_down(xb, a), b, scale
+            return self._combine(adapters)
         # the key holds the adapter tensors themselves (an id() of a freed tensor can be
         # reused) and their in-place version counters
         key = [(A, B, float(s), A._version, B._version) for A, B, s in adapters]
@@ -160,7 +158,15 @@ class FP8Linear(nn.Module):
         if not hit:
             self._lora_cache = self._combine(adapters)
             self._lora_cache_key = key
-        a, b, scale = self._lora_cache
+        return self._lora_cache
+
+    def _lora_operands(self, x2d: torch.Tensor):
+        """(t = bf16(x A^T), B, scale) for the fused epilogue, or (None, None, 0.0)."""
+        ab = self._lora_ab()
+        if ab is None:
+            return None, None, 0.0
+        a, b, scale = ab
+        xb = x2d if x2d.dtype == torch.bfloat16 else x2d.to(torch.bfloat16)
         return ops.lora_down(xb, a), b, scale
 
     @classmethod
@@ -189,20 +195,36 @@ class FP8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape
         x2d = x.reshape(-1, self.in_features)
-        x8, x_scale = quantize_rows(x2d)
         if self.adapters and x.dtype != torch.bfloat16:
             # The reference converts the bf16 linear output to x's dtype and adds each LoRA
             # branch in that dtype (fp8_linear.py:105-108); the fused epilogue adds in bf16,
             # so other dtypes take the reference's sequence (then the folded tanh-GELU).
+            x8, x_scale = quantize_rows(x2d)
             out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, ACT_NONE, None, None, 0.0)
             out = apply_lora_adapters(x2d, out.to(x.dtype), self.adapters)
             if self.act == ACT_GELU_TANH:
                 out = torch.nn.functional.gelu(out, approximate="tanh")
             return out.reshape(*orig_shape[:-1], self.out_features)
+        x8, x_scale = quantize_rows(x2d)
         lora_t, lora_b, lora_scale = self._lora_operands(x2d)
         out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
                                lora_scale)
         return out.reshape(*orig_shape[:-1], self.out_features).to(x.dtype)
+
+    def forward_adaln(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6,
+                      eager_rounding: bool = False) -> torch.Tensor:
+        """``forward`` of the adaLN modulation y = LayerNorm(x) * (1 + scale) + shift of a DiT
+        block's hidden state x [B, S, C] bf16 (shift / scale [B, C] bf16; an extension with
+        no counterpart in the reference, see ``adaln_quantize_rows``) -> [B, S, N] bf16.  The
+        modulation runs inside the activation quantizer; y reaches memory only when LoRA
+        adapters need it for their down-projection.  Equals ``forward(y)`` bit for bit."""
+        if x.ndim != 3 or x.shape[2] != self.in_features:
+            raise ValueError(f"forward_adaln: expected x [B, S, {self.in_features}]")
+        B, S, _ = x.shape
+        lora = bool(self.adapters)
+        x8, sa, y = ops.adaln_quant_rows(x, shift, scale, float(eps), bool(eager_rounding), lora)
+        out = self.forward_quantized(x8, sa, y if lora else None)
+        return out.reshape(B, S, self.out_features)
 
     def forward_quantized(self, x8: torch.Tensor, x_scale: torch.Tensor,
                           x_modulated: torch.Tensor | None = None) -> torch.Tensor:

@@ -295,6 +295,30 @@ def test_lora_down_matches_bf16_matmul():
         np.testing.assert_allclose(t, ref, rtol=2 ** -7, atol=1e-3 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("rank", [0, 64, 128])
+def test_forward_adaln_equals_forward_of_modulation(fl, rank):
+    """FP8Linear.forward_adaln(x, shift, scale) == FP8Linear.forward(y) bit for bit, with no
+    adapter and with rank-64 / rank-128 adapters."""
+    _say(f"forward_adaln rank={rank}")
+    rng = np.random.default_rng(40 + rank)
+    B, S, C, N = 2, 100, 3072, 768
+    lin = torch.nn.Linear(C, N, bias=True).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(to_gpu(bf16_randn(rng, (N, C), 0.02)))
+    mod = fl.FP8Linear.from_linear(lin)
+    if rank:
+        mod.adapters.append((to_gpu(bf16_randn(rng, (rank, C), 0.01)), to_gpu(bf16_randn(rng, (N, rank), 0.01)),
+                             0.5))
+    x = to_gpu(bf16_randn(rng, (B, S, C)))
+    shift, scale = to_gpu(bf16_randn(rng, (B, C), 0.1)), to_gpu(bf16_randn(rng, (B, C), 0.1))
+    out = mod.forward_adaln(x, shift, scale)
+    _, _, y = fl.adaln_quantize_rows(x, shift, scale, return_modulated=True)
+    ref = mod(y.view(B, S, C))
+    torch.cuda.synchronize()
+    assert out.shape == (B, S, N)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("M,N,K,r,gelu", [
     (300, 640, 768, 64, False),      # 128 x 128 tiles, one 64-column LoRA chunk in LDS
     (1100, 1280, 528, 128, True),    # K tail stage, two LoRA chunks, GELU on the bf16 output

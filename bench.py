@@ -44,6 +44,7 @@ import json
 import math
 import os
 import platform
+import re
 import sys
 import time
 
@@ -307,6 +308,158 @@ def cpu_baseline(step_lin: float, step_att: float, runs: int = 5) -> dict:
     }
 
 
+# ---------------------------------------------------------------------------------------
+# Profile summaries (no GPU needed): tables from rocprofv3's CSV output of this script's
+# default workload, e.g.
+#   rocprofv3 --kernel-trace --stats --output-format csv -d T -o run -- python3 bench.py ...
+#   python3 bench.py --summarize-trace T
+#   rocprofv3 --pmc <counters> --output-format csv -d P1 -o run -- python3 bench.py ...   (per pass)
+#   python3 bench.py --summarize-counters P1 P2 P3 P4
+# ---------------------------------------------------------------------------------------
+
+def _csv_rows(directory: str, suffix: str):
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _labels(dispatches, tokens: int = TOKENS):
+    """dispatch id -> part name for the DiT-block kernels of this script's steps, in dispatch
+    order: the three no-activation GEMMs of a step are QKV, attention-out, MLP-down (MLP-up
+    is the GELU instance); activation quantizers are told from the weight quantizers at
+    set-up by their grid (one 256-thread block per 4 rows of the workload's tokens)."""
+    act_grid = str(math.ceil(tokens / 4) * 256)
+    out, k = {}, 0
+    for d, name, grid in dispatches:
+        if "gemm_fp8_rowwise_kernel" in name:
+            act = re.search(r"GemmCfg<[^>]*>, (\d+),", name)
+            if act and act.group(1) == "1":  # the GELU-tanh epilogue
+                out[d] = "gemm[mlp_up]"
+            else:
+                out[d] = ("gemm[qkv]", "gemm[attn_out]", "gemm[mlp_down]")[k % 3]
+                k += 1
+        elif "quant_rows_reg_kernel" in name and grid == act_grid:
+            out[d] = "quant_rows<0, 24>[mlp_down]" if "<0, 24>" in name else "quant_rows<0, 6>"
+        elif "adaln_quant_rows_kernel" in name:
+            out[d] = "adaln_quant_rows"
+        elif "lora_down_kernel" in name:
+            out[d] = "lora_down"
+        elif "attn_fwd_kernel" in name or "attn_fwd_resident_kernel" in name:
+            out[d] = "attn_fwd"
+        elif "attn_kv_colreduce_kernel" in name:
+            out[d] = "attn_quant_kv: colreduce"
+        elif "attn_kv_fold_kernel" in name:
+            out[d] = "attn_quant_kv: fold"
+        elif "attn_quant_kv_kernel" in name:
+            out[d] = "attn_quant_kv: quantize"
+        elif "vectorized_elementwise_kernel" in name and "neg_kernel" in name:
+            out[d] = "torch.neg 1 GiB (HBM reference)"
+    return out
+
+
+PART_ORDER = ("gemm[qkv]", "gemm[attn_out]", "gemm[mlp_up]", "gemm[mlp_down]", "quant_rows<0, 6>",
+              "quant_rows<0, 24>[mlp_down]", "adaln_quant_rows", "lora_down", "attn_quant_kv: colreduce", "attn_quant_kv: fold",
+              "attn_quant_kv: quantize", "attn_fwd", "torch.neg 1 GiB (HBM reference)")
+
+
+def summarize_trace(directory: str, workload: str = "dit480") -> str:
+    """Kernel-trace durations of each part over every step the run made (workload: the
+    --workload of the traced run), and the roofline fraction of its largest attention
+    recomputed from the median launch (for several attentions per step, of all of them)."""
+    _, tokens, _, attns, _ = WORKLOADS[workload]
+    rows = _csv_rows(directory, "kernel_trace.csv")
+    disp = [(int(r["Dispatch_Id"]), r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X"))) for r in rows]
+    lab = _labels(disp, tokens or TOKENS)
+    dur = {}
+    for r in rows:
+        d = int(r["Dispatch_Id"])
+        if d in lab:
+            dur.setdefault(lab[d], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    def median(v):
+        v = sorted(v)
+        return v[len(v) // 2] if len(v) % 2 else 0.5 * (v[len(v) // 2 - 1] + v[len(v) // 2])
+
+    lines = ["| part | launches | median us | mean us | min us | max us |", "|---|---|---|---|---|---|"]
+    for p in PART_ORDER:
+        if p in dur:
+            v = dur[p]
+            lines.append(f"| `{p}` | {len(v)} | {median(v):.1f} | {sum(v) / len(v):.1f} | {min(v):.1f} | "
+                         f"{max(v):.1f} |")
+    if "attn_fwd" in dur and len(attns) == 1:
+        med = median(dur["attn_fwd"])
+        _, b, sq, sk, _ = attns[0]
+        f = attn_flops(b, HEADS, sq, sk, HEAD_DIM)
+        lines += ["", f"Roofline entry recomputed from this trace: attention FLOPs 4 x {b} x 24 x {sq} x {sk} x 128 = "
+                      f"{f / 1e12:.4f} TFLOP per launch / {med:.1f} us (median launch) = "
+                      f"{f / (med * 1e-6) / 1e12:.1f} TFLOP/s = {f / (med * 1e-6) / 1e12 / PEAK_FP8_TFLOPS:.4f} "
+                      f"of the {PEAK_FP8_TFLOPS:.0f} TFLOP/s dense FP8 peak."]
+    return "\n".join(lines)
+
+
+def summarize_counters(directories: list[str]) -> str:
+    """Per part, the mean over its launches of each counter the passes collected, as busy
+    fractions (SQ counters) and calibrated HBM bytes (FETCH_SIZE / WRITE_SIZE)."""
+    per = {}
+    for d in directories:
+        rows = _csv_rows(d, "counter_collection.csv")
+        names = {}
+        vals = {}
+        for r in rows:
+            i = int(r["Dispatch_Id"])
+            names[i] = (r["Kernel_Name"], r["Grid_Size"])
+            vals.setdefault(i, {}).setdefault(r["Counter_Name"], 0.0)
+            vals[i][r["Counter_Name"]] += float(r["Counter_Value"])
+        lab = _labels([(i, n, g) for i, (n, g) in sorted(names.items())])
+        for i, part in lab.items():
+            for c, v in vals[i].items():
+                per.setdefault(part, {}).setdefault(c, []).append(v)
+
+    def m(part, c):
+        v = per.get(part, {}).get(c)
+        return sum(v) / len(v) if v else None
+
+    ref = "torch.neg 1 GiB (HBM reference)"
+    fetch_k = (1 << 30) / (m(ref, "FETCH_SIZE") * 1024) if m(ref, "FETCH_SIZE") else None
+    write_k = (1 << 30) / (m(ref, "WRITE_SIZE") * 1024) if m(ref, "WRITE_SIZE") else None
+    lines = []
+    if fetch_k and write_k:
+        lines += [f"Calibration (the 1 GiB bf16 negation reads and writes exactly 1 GiB per launch): bytes read = "
+                  f"{fetch_k:.3f} x FETCH_SIZE KiB x 1024, bytes written = {write_k:.3f} x WRITE_SIZE KiB x 1024.", ""]
+    lines += ["| part | kernel cycles (M) | MFMA busy | VALU busy | MFMA+VALU co-issue | LDS busy | wait | "
+              "VALU instr / MFMA instr | HBM read MB | HBM write MB |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    for p in PART_ORDER:
+        if p not in per:
+            continue
+        busy = m(p, "SQ_BUSY_CYCLES")
+        cyc = busy / 32 if busy else None  # SQ busy cycles are summed over the 32 shader engines
+        simd = 1024 * cyc if cyc else None  # 256 CUs x 4 SIMDs
+
+        def frac(c, k=1.0):
+            v = m(p, c)
+            return f"{k * v / simd:.1%}" if v is not None and simd else "-"
+        waves = m(p, "SQ_WAVE_CYCLES")
+        wait = f"{m(p, 'SQ_WAIT_INST_ANY') / waves:.1%}" if waves and m(p, "SQ_WAIT_INST_ANY") is not None else "-"
+        ratio = "-"
+        if m(p, "SQ_INSTS_VALU") is not None and m(p, "SQ_INSTS_MFMA"):
+            ratio = f"{m(p, 'SQ_INSTS_VALU') / m(p, 'SQ_INSTS_MFMA'):.1f}"
+        rd = f"{m(p, 'FETCH_SIZE') * 1024 * fetch_k / 1e6:.1f}" if m(p, "FETCH_SIZE") is not None and fetch_k else "-"
+        wr = f"{m(p, 'WRITE_SIZE') * 1024 * write_k / 1e6:.1f}" if m(p, "WRITE_SIZE") is not None and write_k else "-"
+        lines.append(f"| `{p}` | {cyc / 1e6:.2f} | {frac('SQ_VALU_MFMA_BUSY_CYCLES')} | "
+                     f"{frac('SQ_ACTIVE_INST_VALU', 4.0)} | {frac('SQ_VALU_MFMA_COEXEC_CYCLES')} | "
+                     f"{frac('SQ_ACTIVE_INST_LDS', 4.0)} | {wait} | {ratio} | {rd} | {wr} |"
+                     if cyc else f"| `{p}` | - | - | - | - | - | - | {ratio} | {rd} | {wr} |")
+    lines += ["", "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles); VALU busy = 4 x "
+                  "SQ_ACTIVE_INST_VALU (quad-cycles) / the same; co-issue = SQ_VALU_MFMA_COEXEC_CYCLES / the same; "
+                  "LDS busy = 4 x SQ_ACTIVE_INST_LDS / the same; kernel cycles = SQ_BUSY_CYCLES / 32; wait = "
+                  "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."]
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,7 +472,17 @@ def main() -> int:
     ap.add_argument("--repair-tau", type=float, default=-1.0,
                     help="exact repair of P codes >= tau in every attention (the reference's quality "
                          "profile uses 0.5); < 0 disables it (default)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print the per-part table of a rocprofv3 --kernel-trace run of this script and exit")
+    ap.add_argument("--summarize-counters", metavar="DIR", nargs="+",
+                    help="print the per-part counter table of rocprofv3 --pmc runs of this script and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.workload))
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)

@@ -59,10 +59,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over this script's dispatches and
 # scaled by what the counters read for the 1 GiB streaming kernel of
 # hbm_stream_reference() (FETCH_SIZE reports 0.500 of the bytes read, WRITE_SIZE 1.000 of
-# the bytes written): 361743.8 KiB x 2 fetched + 123661.0 KiB written.  The algorithmic
+# the bytes written): 358747.9 KiB x 2 fetched + 121680.1 KiB written.  The algorithmic
 # traffic is 249.2 MB of bf16 Q (quantized inside the launch) and K8/V8T read + 124.6 MB
 # of output written.
-ATTN_TRAFFIC_BYTES = 361743.8 * 1024 * 2 + 123661.0 * 1024
+ATTN_TRAFFIC_BYTES = 358747.9 * 1024 * 2 + 121680.1 * 1024
 TOKENS = 20280                # 13 x 30 x 52
 HIDDEN, MLP = 3072, 12288
 HEADS, HEAD_DIM = 24, 128
@@ -327,13 +327,18 @@ def _csv_rows(directory: str, suffix: str):
         return list(csv.DictReader(f))
 
 
-def _labels(dispatches, tokens: int = TOKENS):
+def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
     """dispatch id -> part name for the DiT-block kernels of this script's steps, in dispatch
     order: the three no-activation GEMMs of a step are QKV, attention-out, MLP-down (MLP-up
     is the GELU instance); activation quantizers are told from the weight quantizers at
     set-up by their grid (one 256-thread block per 4 rows of the workload's tokens)."""
     act_grid = str(math.ceil(tokens / 4) * 256)
     out, k = {}, 0
+    na = len(attn_names)
+    ka = kq = 0  # attention launches and K/V quantizer folds so far (a step runs them in order)
+
+    def sfx(i):
+        return "" if na == 1 else f"[{attn_names[i % na]}]"
     for d, name, grid in dispatches:
         if "gemm_fp8_rowwise_kernel" in name:
             act = re.search(r"GemmCfg<[^>]*>, (\d+),", name)
@@ -349,13 +354,15 @@ def _labels(dispatches, tokens: int = TOKENS):
         elif "lora_down_kernel" in name:
             out[d] = "lora_down"
         elif "attn_fwd_kernel" in name or "attn_fwd_resident_kernel" in name:
-            out[d] = "attn_fwd"
+            out[d] = "attn_fwd" + sfx(ka)
+            ka += 1
         elif "attn_kv_colreduce_kernel" in name:
-            out[d] = "attn_quant_kv: colreduce"
+            out[d] = "attn_quant_kv: colreduce" + sfx(kq)
         elif "attn_kv_fold_kernel" in name:
-            out[d] = "attn_quant_kv: fold"
+            out[d] = "attn_quant_kv: fold" + sfx(kq)
         elif "attn_quant_kv_kernel" in name:
-            out[d] = "attn_quant_kv: quantize"
+            out[d] = "attn_quant_kv: quantize" + sfx(kq)
+            kq += 1
         elif "vectorized_elementwise_kernel" in name and "neg_kernel" in name:
             out[d] = "torch.neg 1 GiB (HBM reference)"
     return out
@@ -372,8 +379,9 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
     recomputed from the median launch (for several attentions per step, of all of them)."""
     _, tokens, _, attns, _ = WORKLOADS[workload]
     rows = _csv_rows(directory, "kernel_trace.csv")
-    disp = [(int(r["Dispatch_Id"]), r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X"))) for r in rows]
-    lab = _labels(disp, tokens or TOKENS)
+    disp = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X"))) for r in rows)
+    names = tuple(a[0] for a in attns)
+    lab = _labels(disp, tokens or TOKENS, names)
     dur = {}
     for r in rows:
         d = int(r["Dispatch_Id"])
@@ -383,20 +391,27 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
         v = sorted(v)
         return v[len(v) // 2] if len(v) % 2 else 0.5 * (v[len(v) // 2 - 1] + v[len(v) // 2])
 
+    order = list(PART_ORDER)
+    if len(names) > 1:
+        order += [f"{base}[{n}]" for n in names for base in ("attn_quant_kv: colreduce", "attn_quant_kv: fold",
+                                                              "attn_quant_kv: quantize", "attn_fwd")]
     lines = ["| part | launches | median us | mean us | min us | max us |", "|---|---|---|---|---|---|"]
-    for p in PART_ORDER:
+    for p in order:
         if p in dur:
             v = dur[p]
             lines.append(f"| `{p}` | {len(v)} | {median(v):.1f} | {sum(v) / len(v):.1f} | {min(v):.1f} | "
                          f"{max(v):.1f} |")
-    if "attn_fwd" in dur and len(attns) == 1:
-        med = median(dur["attn_fwd"])
-        _, b, sq, sk, _ = attns[0]
+    lines.append("")
+    for i, (name, b, sq, sk, _) in enumerate(attns):
+        key = "attn_fwd" + ("" if len(attns) == 1 else f"[{name}]")
+        if key not in dur:
+            continue
+        med = median(dur[key])
         f = attn_flops(b, HEADS, sq, sk, HEAD_DIM)
-        lines += ["", f"Roofline entry recomputed from this trace: attention FLOPs 4 x {b} x 24 x {sq} x {sk} x 128 = "
-                      f"{f / 1e12:.4f} TFLOP per launch / {med:.1f} us (median launch) = "
-                      f"{f / (med * 1e-6) / 1e12:.1f} TFLOP/s = {f / (med * 1e-6) / 1e12 / PEAK_FP8_TFLOPS:.4f} "
-                      f"of the {PEAK_FP8_TFLOPS:.0f} TFLOP/s dense FP8 peak."]
+        lines.append(f"`{key}` recomputed from this trace: FLOPs 4 x {b} x 24 x {sq} x {sk} x 128 = {f / 1e12:.4f} "
+                     f"TFLOP per launch / {med:.1f} us (median launch) = {f / (med * 1e-6) / 1e12:.1f} TFLOP/s = "
+                     f"{f / (med * 1e-6) / 1e12 / PEAK_FP8_TFLOPS:.4f} of the {PEAK_FP8_TFLOPS:.0f} TFLOP/s dense "
+                     f"FP8 peak.")
     return "\n".join(lines)
 
 

@@ -1,7 +1,6 @@
 // Per-row pieces of the activation quantizers, for a bf16 row held by one wave: NC 16-byte
 // chunks per lane, chunk c of lane l holding elements [(c * 64 + l) * 8, +8) (chunks past the
-// row's end hold zeros).  Used by adaln_quant_rows_kernel and the quantizers with the LoRA
-// down-projection fused.
+// row's end hold zeros).  Used by adaln_quant_rows_kernel.
 #pragma once
 
 #include "common.h"

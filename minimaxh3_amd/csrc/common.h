@@ -107,25 +107,30 @@ __device__ __forceinline__ float e4m3_scale(float amax) {
 
 // Correctly rounded x / s given r = RN(1/s): q0 = RN(x r) is faithful, the remainder
 // x - s q0 is exact with an fma, and RN(q0 + rem * r) is RN(x / s) (Markstein's
-// theorem, binary fp32, no overflow; quotients here are bounded by ~448).  The sign is
-// copied back because for x = -0 the remainder step yields +0 (IEEE -0 / s is -0).
-// For s = +inf (a block maximum of inf) r is 0: with s capped at the largest finite value
-// in the remainder step, a finite x gives +-0 (IEEE x / inf) and +-inf or NaN gives NaN.
+// theorem, binary fp32, no overflow; quotients here are bounded by ~448).  The remainder
+// is taken negated, nrem = RN(s q0 - x) = -rem, and the last step is RN(nrem * -r + q0):
+// the same value for every x != 0, and for x = -0 the sum -0 + -0 keeps the sign of IEEE
+// -0 / s (the positive remainder would give +0).  For s = +inf (a block maximum of inf)
+// r is 0: with s capped at the largest finite value in the remainder step, a finite x
+// gives +-0 (IEEE x / inf) and +-inf or NaN gives NaN.
 __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
-  float q0 = x * r;
-  float rem = __builtin_fmaf(-q0, fminf(s, 3.40282347e38f), x);
-  return __builtin_copysignf(__builtin_fmaf(rem, r, q0), x);
+  const float q0 = x * r;
+  const float nrem = __builtin_fmaf(q0, fminf(s, 3.40282347e38f), -x);
+  return __builtin_fmaf(nrem, -r, q0);
 }
 
 __device__ __forceinline__ float clamp448(float q) { return fminf(fmaxf(q, -kE4m3Max), kE4m3Max); }
 
-// Two fp32 values -> two e4m3fn bytes (RNE, hardware conversion) in the low 16 bits.
+// Two fp32 values -> two e4m3fn bytes (RNE, hardware conversion) in the low 16 bits.  The
+// conversion writes one half of its destination and keeps the other from its last operand;
+// a's own bits stand in there (the half is masked off or overwritten), so no zeroed
+// register has to be made for it.
 __device__ __forceinline__ uint32_t cvt2_e4m3(float a, float b) {
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false) & 0xffffu;
 }
 // Four fp32 values -> four e4m3fn bytes packed little-endian in one dword.
 __device__ __forceinline__ uint32_t cvt4_e4m3(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }

@@ -22,8 +22,116 @@ namespace mxf8 {
 // lane (chunk c of lane l covers elements [(c*64 + l) * E, +E)).  Requires K % E == 0
 // and 16-byte aligned rows.  All of the row's loads are issued before the first use (a
 // loop that folds each chunk into the max as it arrives measured 3-19% slower).
+//
+// The row maximum compares absolute-value bit patterns as integers (two 16-bit ones per
+// v_pk_max_u16): for every non-NaN value the order of |x| is the order of its pattern
+// with the sign cleared, and NaN patterns lie above inf's.  A row whose largest pattern is
+// a NaN takes the float maximum instead, which skips NaN as the reference's tl.max does.
+// The codes are then made and stored chunk by chunk.
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+template <int DT>
+struct RowBits;
+template <>
+struct RowBits<MXF8_BF16> {
+  static constexpr uint32_t kInf = 0x7f80u;
+  static __device__ __forceinline__ float to_f32(uint32_t b) { return bf16_bits_to_f32(b); }
+};
+template <>
+struct RowBits<MXF8_F16> {
+  static constexpr uint32_t kInf = 0x7c00u;
+  static __device__ __forceinline__ float to_f32(uint32_t b) { return f16_bits_to_f32(b); }
+};
+template <>
+struct RowBits<MXF8_F32> {
+  static constexpr uint32_t kInf = 0x7f800000u;
+  static __device__ __forceinline__ float to_f32(uint32_t b) { return __uint_as_float(b); }
+};
+
+// Largest |x| pattern of this lane's chunks.
 template <int DT, int NC>
-__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const void* __restrict__ x, int64_t M, int64_t K,
+__device__ __forceinline__ uint32_t chunk_absmax_bits(const uint4 (&v)[NC]) {
+  if constexpr (DT == MXF8_F32) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = max(m, w[i] & 0x7fffffffu);
+    }
+    return m;
+  } else {
+    v2u16 m = {0, 0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(v2u16, w[i] & 0x7fff7fffu));
+    }
+    return max((uint32_t)m[0], (uint32_t)m[1]);
+  }
+}
+
+// Largest |x| pattern of this lane's chunks with NaN skipped (for rows that hold a NaN).
+// Integer work only: float conversions here would be shared with the code loop's and
+// held in registers across the maximum.
+template <int DT, int NC>
+__device__ __forceinline__ uint32_t chunk_absmax_bits_nonan(const uint4 (&v)[NC]) {
+  constexpr uint32_t kInf = RowBits<DT>::kInf;
+  uint32_t m = 0;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == MXF8_F32) {
+        const uint32_t b = w[i] & 0x7fffffffu;
+        m = max(m, b <= kInf ? b : 0u);
+      } else {
+        const uint32_t b0 = w[i] & 0x7fffu, b1 = (w[i] >> 16) & 0x7fffu;
+        m = max(m, max(b0 <= kInf ? b0 : 0u, b1 <= kInf ? b1 : 0u));
+      }
+    }
+  }
+  return m;
+}
+
+// The e4m3 codes of one chunk (E elements) at orow + idx * E.
+template <int DT>
+__device__ __forceinline__ void chunk_store_codes(const uint4& q, int64_t idx, float s, float r,
+                                                  uint8_t* __restrict__ orow) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (DT == MXF8_F32) {
+    float f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = clamp448(div_by_scale(__uint_as_float(w[i]), s, r));
+    *reinterpret_cast<uint32_t*>(orow + idx * 4) = cvt4_e4m3(f[0], f[1], f[2], f[3]);
+  } else {
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = clamp448(div_by_scale(Elem<DT>::lo(w[i]), s, r));
+      f[2 * i + 1] = clamp448(div_by_scale(Elem<DT>::hi(w[i]), s, r));
+    }
+    *reinterpret_cast<uint2*>(orow + idx * 8) = make_uint2(cvt4_e4m3(f[0], f[1], f[2], f[3]),
+                                                           cvt4_e4m3(f[4], f[5], f[6], f[7]));
+  }
+}
+
+// FULL: every lane's NC chunks lie inside the row (K = NC * 64 * E), so no chunk is tested.
+// Waves per SIMD asked of the register allocator for whole bf16 rows (the row takes 4 NC
+// registers; without a target the scheduler spends registers on early conversions, down
+// to two waves at NC = 24).  The other variants keep the allocator's choice, which a
+// target this tight would turn into spills.
+template <int DT, int NC, bool FULL>
+constexpr int quant_rows_waves() {
+  if (DT != MXF8_BF16 || !FULL) return 1;
+  return NC <= 8 ? 8 : NC <= 12 ? 6 : NC <= 16 ? 5 : NC <= 24 ? 4 : 3;
+}
+
+template <int DT, int NC, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(quant_rows_waves<DT, NC, FULL>())))
+void quant_rows_reg_kernel(const void* __restrict__ x, int64_t M, int64_t K,
                                                              int64_t ldx, uint8_t* __restrict__ x8,
                                                              float* __restrict__ scale) {
   typedef typename Elem<DT>::T T;
@@ -34,50 +142,30 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const void* __restr
   const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const T*>(x) + row * ldx);
   const int64_t nchunk = K / E;
   uint4 v[NC];
+  if constexpr (FULL) {
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
-  }
-  float amax = 0.0f;
+    for (int c = 0; c < NC; ++c) v[c] = xr[c * 64 + lane];
+  } else {
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == MXF8_F32) {
-        amax = fmaxf(amax, fabsf(__uint_as_float(w[i])));
-      } else {
-        amax = fmaxf(amax, fmaxf(fabsf(Elem<DT>::lo(w[i])), fabsf(Elem<DT>::hi(w[i]))));
-      }
+    for (int c = 0; c < NC; ++c) {
+      const int64_t idx = (int64_t)c * 64 + lane;
+      v[c] = idx < nchunk ? xr[idx] : make_uint4(0, 0, 0, 0);
     }
   }
-  amax = wave_max(amax);
+  uint32_t mb = chunk_absmax_bits<DT, NC>(v);
+  if (__builtin_amdgcn_ballot_w64(mb > RowBits<DT>::kInf)) mb = chunk_absmax_bits_nonan<DT, NC>(v);
+  const float amax = wave_max(RowBits<DT>::to_f32(mb));
   const float s = e4m3_scale(amax);
   const float r = __fdiv_rn(1.0f, s);
   uint8_t* orow = x8 + row * K;
+  if constexpr (FULL) {
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int64_t idx = (int64_t)c * 64 + lane;
-    if (idx < nchunk) {
-      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-      if constexpr (DT == MXF8_F32) {
-        float f[4];
+    for (int c = 0; c < NC; ++c) chunk_store_codes<DT>(v[c], c * 64 + lane, s, r, orow);
+  } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = clamp448(div_by_scale(__uint_as_float(w[i]), s, r));
-        *reinterpret_cast<uint32_t*>(orow + idx * 4) = cvt4_e4m3(f[0], f[1], f[2], f[3]);
-      } else {
-        float f[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f[2 * i] = clamp448(div_by_scale(Elem<DT>::lo(w[i]), s, r));
-          f[2 * i + 1] = clamp448(div_by_scale(Elem<DT>::hi(w[i]), s, r));
-        }
-        uint2 o;
-        o.x = cvt4_e4m3(f[0], f[1], f[2], f[3]);
-        o.y = cvt4_e4m3(f[4], f[5], f[6], f[7]);
-        *reinterpret_cast<uint2*>(orow + idx * 8) = o;
-      }
+    for (int c = 0; c < NC; ++c) {
+      const int64_t idx = (int64_t)c * 64 + lane;
+      if (idx < nchunk) chunk_store_codes<DT>(v[c], idx, s, r, orow);
     }
   }
   if (lane == 0) scale[row] = s;
@@ -113,7 +201,11 @@ __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
 template <int DT, int NC>
 static void launch_quant_rows_reg(const void* x, int64_t M, int64_t K, int64_t ldx, uint8_t* x8, float* scale,
                                   hipStream_t st) {
-  quant_rows_reg_kernel<DT, NC><<<dim3((unsigned)cdiv(M, 4)), dim3(256), 0, st>>>(x, M, K, ldx, x8, scale);
+  const dim3 grid((unsigned)cdiv(M, 4));
+  if (K == (int64_t)NC * 64 * (16 / (DT == MXF8_F32 ? 4 : 2)))
+    quant_rows_reg_kernel<DT, NC, true><<<grid, dim3(256), 0, st>>>(x, M, K, ldx, x8, scale);
+  else
+    quant_rows_reg_kernel<DT, NC, false><<<grid, dim3(256), 0, st>>>(x, M, K, ldx, x8, scale);
 }
 
 template <int DT>

@@ -387,28 +387,117 @@ struct AttnPB {
   v8i lo[REP ? 2 : 1];
 };
 
-// A run of matrix-core products with their A fragments fetched from LDS three products
-// ahead (four fragments in flight), so the products issue back to back instead of each
-// waiting for its own LDS read.  The run is the PV products of one tile (when PV: O^T tile
-// x of key half kh, or the row-sum product when x == D/32; with REP each fragment also
-// multiplies the two repair parts) followed by the QK^T products of another (when QK:
-// subtile u, half hh).
-template <int D, bool PV, bool QK, int AHEAD = 3>
+// Per-tile constants of the code arithmetic (see attn_codes_w4).
+struct AttnCodeK {
+  float c8, cst, c8f, cstf, tau;
+  template <bool HAS_BIAS>
+  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float m_new, float tau) {
+    AttnCodeK k;
+    k.cst = 56.0f - 8.0f * m_new;
+    k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
+    k.c8f = k.c8 * 0x1p64f;
+    k.cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
+    k.tau = tau;
+    return k;
+  }
+};
+
+// The exp2-free P codes of scores 4 w4 .. 4 w4 + 3 of score subtile t: word 4 (t & 1) + w4
+// of the PV B operand of key half t >> 1.
+//
+// code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
+// 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
+// inactive.  Three FMAs per score, all at the full FMA rate:
+//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
+//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
+//   t    = fma(bits, keep, 1.5 * 2^23)
+// keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
+// is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
+// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
+// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
+// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
+//
+// Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
+// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
+// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
+// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
+// hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
+// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
+// significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
+// lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
+template <bool REP>
+__device__ __forceinline__ void attn_codes_w4(const v16f& st, const AttnCodeK& k, int t, int w4, AttnPB<REP>& pb) {
+  {
+    uint32_t tb[4];
+    float bits[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = st[4 * w4 + e];
+      bits[e] = __builtin_fmaf(x, k.c8, k.cst);
+      const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, k.c8f, k.cstf), 0.0f, 1.0f);
+      tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
+    }
+    // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
+    const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
+                          __builtin_amdgcn_perm(tb[3], tb[2], 0x04000c0cu);
+    // An empty use keeps the codes here instead of letting them sink to their consumer
+    // (the PV products): a reordered tile would hold the scores and the codes live together.
+    asm volatile("" ::"v"(word));
+    pb.p[t >> 1][4 * (t & 1) + w4] = (int)word;
+    if constexpr (REP) {
+      const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+      const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
+      const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
+      float d8[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
+        const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
+        const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
+        d8[e] = papx[e] >= k.tau ? d : 0.0f;
+      }
+      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
+      const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+      const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
+      pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
+      pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
+    }
+  }
+}
+
+// The codes of score subtile t.
+template <bool REP>
+__device__ __forceinline__ void attn_codes_sub(const v16f& st, const AttnCodeK& k, int t, AttnPB<REP>& pb) {
+#pragma unroll
+  for (int w4 = 0; w4 < 4; ++w4) attn_codes_w4<REP>(st, k, t, w4, pb);
+}
+
+// A run of matrix-core products with their A fragments fetched from LDS AHEAD products
+// ahead (AHEAD + 1 fragments in flight), so the products issue back to back instead of
+// each waiting for its own LDS read.  The run is the PV products of key halves
+// [KH0, KH1) of one tile (per half: O^T tile x for x < D/32, then the row-sum product at
+// x == D/32; with REP each fragment also multiplies the two repair parts) followed by the
+// QK^T products of score subtiles [U0, U1) of another (per subtile: the D/64 channel
+// halves hh).
+template <int D, int KH0, int KH1, int U0, int U1, int AHEAD = 3>
 struct AttnMfmaRun {
   static constexpr int RING = AHEAD + 1;
   static constexpr int NDT = D / 32, QKM = D / 64;
-  static constexpr int NPV = PV ? 2 * (NDT + 1) : 0, NQK = QK ? 4 * QKM : 0, N = NPV + NQK;
+  static constexpr int NPV = (KH1 - KH0) * (NDT + 1), NQK = (U1 - U0) * QKM, N = NPV + NQK;
 
   template <int K>
   __device__ static __forceinline__ v8i frag(const uint8_t* sV, const uint8_t* sK, const AttnFragOfs<D>& fo) {
     if constexpr (K < NPV) {
-      constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
+      constexpr int kh = KH0 + K / (NDT + 1), x = K % (NDT + 1);
       if constexpr (x == NDT)
         return fo.rowsum_sel;
       else
         return lds_pair(sV + x * 32 * 128, fo.v[kh][0], fo.v[kh][1]);
     } else {
-      constexpr int u = (K - NPV) / QKM, hh = (K - NPV) % QKM;
+      constexpr int u = U0 + (K - NPV) / QKM, hh = (K - NPV) % QKM;
       return lds_pair(sK + u * 32 * D, fo.k[hh][0], fo.k[hh][1]);
     }
   }
@@ -417,7 +506,7 @@ struct AttnMfmaRun {
   __device__ static __forceinline__ void exec(const v8i& fr, const AttnPB<REP>& pb, const v8i (&qf)[D / 64],
                                               v16f (&s)[4], AttnState<D>& st) {
     if constexpr (K < NPV) {
-      constexpr int kh = K / (NDT + 1), x = K % (NDT + 1);
+      constexpr int kh = KH0 + K / (NDT + 1), x = K % (NDT + 1);
       if constexpr (x == NDT) {
         st.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fr, pb.p[kh], st.lacc, 0, 0, 0, 0, 0, 0);
         if constexpr (REP) {
@@ -436,7 +525,7 @@ struct AttnMfmaRun {
         }
       }
     } else {
-      constexpr int u = (K - NPV) / QKM, hh = (K - NPV) % QKM;
+      constexpr int u = U0 + (K - NPV) / QKM, hh = (K - NPV) % QKM;
       if constexpr (hh == 0) {
         v16f z;
 #pragma unroll
@@ -519,13 +608,14 @@ __device__ __forceinline__ float attn_bias_score(float dot, float sq, float skj,
 
 // Invalid keys (past Sk, masked, bias <= -1e8) get attn_invalid_score; with a bias S is
 // formed explicitly as (dot * sq) * sk + bias * log2 e.
-template <bool HAS_MASK, bool HAS_BIAS>
+// Score subtiles [T0, T0 + NT).
+template <bool HAS_MASK, bool HAS_BIAS, int T0 = 0, int NT = 4>
 __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sAux, int kv0, int Sk, float sq,
                                                  float skj, int lane) {
   const int g = lane >> 5;
   const float vinv = attn_invalid_score<HAS_BIAS>(sq, skj);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = T0; t < T0 + NT; ++t) {
     const int kb = 64 * (t >> 1) + 16 * (t & 1) + 32 * g;
     float bias[16];
     if constexpr (HAS_BIAS) {
@@ -554,37 +644,14 @@ __device__ __forceinline__ void attn_mask_scores(v16f (&s)[4], const uint8_t* sA
   }
 }
 
-// Row max of the tile, the lazy-max decision and the exp2-free P codes.  Returns the new
-// row max m_new of the lane's query; pb.p receives the codes (the PV B operand).
-//
-// code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
-// 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
-// inactive.  Three FMAs per score, all at the full FMA rate:
-//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
-//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
-//   t    = fma(bits, keep, 1.5 * 2^23)
-// keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
-// is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
-// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
-// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
-// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
-//
-// Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
-// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
-// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
-// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
-// hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
-// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
-// significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
-// lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
-// Row max of the tile (exactly the reference's fp32 S max: x -> (x * sq) * sk is monotonic)
-// and the lazy-max decision; returns the new row max m_new of the lane's query.  Four
-// independent v_max3 chains, so that the VALU need not wait on each result.
-template <bool HAS_BIAS>
-__device__ __forceinline__ float attn_tile_max(const v16f (&s)[4], float sq, float skj, float m_old) {
+// Row max over score subtiles [T0, T0 + NT) (exactly the reference's fp32 S max over
+// those keys: x -> (x * sq) * sk is monotonic), floored at -1e9.  Four independent v_max3
+// chains, so that the VALU need not wait on each result.
+template <bool HAS_BIAS, int T0 = 0, int NT = 4>
+__device__ __forceinline__ float attn_part_max(const v16f (&s)[4], float sq, float skj) {
   float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = T0; t < T0 + NT; ++t)
 #pragma unroll
     for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], s[t][i]);
   float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
@@ -594,97 +661,20 @@ __device__ __forceinline__ float attn_tile_max(const v16f (&s)[4], float sq, flo
     const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
     mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   }
-  const float rmax = fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
-  return (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
+  return fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
 }
 
-// Per-tile constants of the code arithmetic (see attn_codes_sub).
-struct AttnCodeK {
-  float c8, cst, c8f, cstf, tau;
-  template <bool HAS_BIAS>
-  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float m_new, float tau) {
-    AttnCodeK k;
-    k.cst = 56.0f - 8.0f * m_new;
-    k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
-    k.c8f = k.c8 * 0x1p64f;
-    k.cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
-    k.tau = tau;
-    return k;
-  }
-};
-
-// The exp2-free P codes of score subtile t (the PV B operand words 4 (t & 1) .. + 3 of half
-// t >> 1).
-//
-// code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
-// 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
-// inactive.  Three FMAs per score, all at the full FMA rate:
-//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
-//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
-//   t    = fma(bits, keep, 1.5 * 2^23)
-// keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
-// is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
-// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
-// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
-// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
-//
-// Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
-// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
-// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
-// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
-// hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
-// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
-// significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
-// lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
-template <bool REP>
-__device__ __forceinline__ void attn_codes_sub(const v16f& st, const AttnCodeK& k, int t, AttnPB<REP>& pb) {
-#pragma unroll
-  for (int w4 = 0; w4 < 4; ++w4) {
-    uint32_t tb[4];
-    float bits[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = st[4 * w4 + e];
-      bits[e] = __builtin_fmaf(x, k.c8, k.cst);
-      const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, k.c8f, k.cstf), 0.0f, 1.0f);
-      tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
-    }
-    // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
-    const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
-                          __builtin_amdgcn_perm(tb[3], tb[2], 0x04000c0cu);
-    // An empty use keeps the codes here instead of letting them sink to their consumer
-    // (the PV products): a reordered tile would hold the scores and the codes live together.
-    asm volatile("" ::"v"(word));
-    pb.p[t >> 1][4 * (t & 1) + w4] = (int)word;
-    if constexpr (REP) {
-      const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
-      const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
-      const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
-      float d8[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
-        const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
-        const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
-        d8[e] = papx[e] >= k.tau ? d : 0.0f;
-      }
-      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
-      const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-      const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
-      pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
-      pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
-    }
-  }
+// The lazy-max decision (kernels/fp8_attention.py:264): the row max moves to the tile's
+// maximum rmax only when that exceeds it by more than 8, or while it is still -1e9.
+__device__ __forceinline__ float attn_lazy_max(float rmax, float m_old) {
+  return (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
 }
 
 // Row max, lazy-max decision and the codes of the whole tile; returns m_new.
 template <bool HAS_BIAS, bool REP>
 __device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, float tau,
                                             AttnPB<REP>& pb) {
-  const float m_new = attn_tile_max<HAS_BIAS>(s, sq, skj, m_old);
+  const float m_new = attn_lazy_max(attn_part_max<HAS_BIAS>(s, sq, skj), m_old);
   const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, m_new, tau);
 #pragma unroll
   for (int t = 0; t < 4; ++t) attn_codes_sub<REP>(s[t], k, t, pb);
@@ -814,13 +804,13 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     const int kv0 = j * 128;
     v16f s[4];
     AttnPB<DO_REPAIR> pb;
-    AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
+    AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
     const float m_new = attn_codes<HAS_BIAS, DO_REPAIR>(s, cx.sqI, skj, st.m, tau, pb);
     if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
     st.m = m_new;
-    AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
+    AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
   }
   AttnSv<D> svr;
@@ -959,14 +949,14 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         const int kv0 = j * 128;
         v16f s[4];
         AttnPB<false> pb;
-        AttnMfmaRun<D, false, true>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
+        AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
         const float m_new = attn_codes<HAS_BIAS, false>(s, cx.sqI, skj, st.m, -1.0f, pb);
         // O and l are still zero on the first tile: rescaling them changes no bit
         if (i > 0 && __builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
         st.m = m_new;
-        AttnMfmaRun<D, true, false>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
+        AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         j = j + 1 == nk ? 0 : j + 1;
       }
     }

@@ -348,7 +348,7 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
                 out[d] = ("gemm[qkv]", "gemm[attn_out]", "gemm[mlp_down]")[k % 3]
                 k += 1
         elif "quant_rows_reg_kernel" in name and grid == act_grid:
-            out[d] = "quant_rows<0, 24>[mlp_down]" if "<0, 24>" in name else "quant_rows<0, 6>"
+            out[d] = "quant_rows<0, 24>[mlp_down]" if "<0, 24" in name else "quant_rows<0, 6>"
         elif "adaln_quant_rows_kernel" in name:
             out[d] = "adaln_quant_rows"
         elif "lora_down_kernel" in name:

@@ -160,21 +160,23 @@ struct AttnCtx {
 
   // The Q quantizer of this work item's 128-row block, fused: q~ = fp32(q) * c, sq =
   // max(max|q~|, 1e-12) / 448 over the block, codes e4m3(clamp(q~ / sq)) -- the arithmetic
-  // of attn_quant_qk_kernel, so fragments and scale are bit-identical to its q8 / sq.
-  // Rows >= Sq quantize as zeros.  red: 4 floats of LDS no DMA writes before the next
-  // attn_barrier.  Ends with a workgroup barrier.
+  // of attn_quant_qk_kernel, so the scale and the fragments of rows < Sq are bit-identical
+  // to its sq / q8.  red: 4 floats of LDS no DMA writes before the next attn_barrier.  Ends
+  // with a workgroup barrier.
   template <int QDT>
   __device__ __forceinline__ void quant_q(const AttnQ16& qa, int Sq, int nq, float* red) {
     uint4 raw[D / 64][4];
     load_q16(qa, b, h, qrow, Sq, lane, raw);
-    quant_q_raw<QDT>(raw, qrow < Sq, qa, nq, red);
+    quant_q_raw<QDT>(raw, qa, nq, red);
   }
 
   // The 16-bit Q values this lane quantizes: row `row` of head (b_, h_), bytes
-  // [64 hh + 32 g, +32) of its codes.  A row >= Sq reads row Sq - 1 and quant_q_raw is told
-  // to take zeros instead: the loads stay unconditional and nothing touches their
-  // registers before they are consumed, so no wait lands where they are issued and no
-  // branch splits the count of loads in flight that later waits rely on.
+  // [64 hh + 32 g, +32) of its codes.  A row >= Sq reads row Sq - 1 (of the same 128-row
+  // block): a copy of one of the block's rows leaves the block maximum as it is, and the
+  // query of a row past Sq is computed but never stored (every statistic of the kernel is
+  // per query), so its codes need no masking.  The loads stay unconditional and nothing
+  // touches their registers before they are consumed, so no wait lands where they are
+  // issued and no branch splits the count of loads in flight that later waits rely on.
   static __device__ __forceinline__ void load_q16(const AttnQ16& qa, int b_, int h_, int row, int Sq, int lane_,
                                                   uint4 (&raw)[D / 64][4]) {
     const int g = lane_ >> 5;
@@ -186,10 +188,8 @@ struct AttnCtx {
       for (int u = 0; u < 4; ++u) raw[hh][u] = *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u);
   }
 
-  // valid = false: the row lies past Sq and quantizes as zeros.
   template <int QDT>
-  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], bool valid, const AttnQ16& qa, int nq,
-                                              float* red) {
+  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], const AttnQ16& qa, int nq, float* red) {
     float f[D / 64][32];
     float amax = 0.0f;
 #pragma unroll
@@ -197,7 +197,7 @@ struct AttnCtx {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const uint4 r = raw[hh][u];
-        const uint32_t w[4] = {valid ? r.x : 0u, valid ? r.y : 0u, valid ? r.z : 0u, valid ? r.w : 0u};
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           f[hh][8 * u + 2 * i] = Elem<QDT>::lo(w[i]) * qa.c;
@@ -926,7 +926,7 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       // quantizes a real tile and writes no scale
       AttnQ16 qx = qa;
       if (!active) qx.sq_out = nullptr;
-      cx.template quant_q_raw<ODT>(rawnext, cx.qrow < Sq, qx, nq, qred + 8 * parity + 4 * grp);
+      cx.template quant_q_raw<ODT>(rawnext, qx, nq, qred + 8 * parity + 4 * grp);
       parity ^= 1;
     } else {
 #pragma unroll

@@ -36,13 +36,21 @@ def _rows_with_non_finite(rng, M, K):
     return x
 
 
-@pytest.mark.parametrize("K", [3072, 100])  # one-wave-per-row path, general path
-def test_quant_rows_non_finite(K):
-    _say(f"quant_rows non-finite K={K}")
+# One wave per row with whole rows in registers (K = 3072 / 12288 bf16, 3072 fp16, 1024 fp32:
+# 64 lanes x 16 bytes x NC chunks exactly), with a partial last chunk (K = 1000, 200), and the
+# general path (K = 100 is not a multiple of the 16-byte chunk).  Each register path has its
+# own NaN-skipping maximum per element type.
+@pytest.mark.parametrize("K,dtype", [(3072, torch.bfloat16), (12288, torch.bfloat16), (1000, torch.bfloat16),
+                                     (3072, torch.float16), (200, torch.float16), (1024, torch.float32),
+                                     (100, torch.bfloat16)])
+def test_quant_rows_non_finite(K, dtype):
+    _say(f"quant_rows non-finite K={K} {dtype}")
     from minimaxh3_amd import ops
     rng = np.random.default_rng(K)
     x = _rows_with_non_finite(rng, 9, K)
-    x8, sa = ops.quant_rows(to_gpu(x))
+    if dtype == torch.float16:
+        x = x.astype(np.float16).astype(np.float32)
+    x8, sa = ops.quant_rows(to_gpu(x, dtype))
     rc, rs = ol.quantize_rows(x)
     np.testing.assert_array_equal(codes(x8), rc)
     np.testing.assert_array_equal(sa.cpu().numpy(), rs)

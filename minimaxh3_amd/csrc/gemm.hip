@@ -11,9 +11,10 @@
 // (BM/WM) x (BN/WN) built from v_mfma_f32_32x32x64_f8f6f4.  The large configuration runs
 // 8 waves on a 256 x 256 tile, two waves per SIMD.  Operand tiles are copied global -> LDS
 // with the direct-to-LDS DMA (buffer_load_dwordx4 ... lds: 64 lanes x 16 bytes = 8 rows x
-// 128 bytes, whole cache lines) into two stage buffers; one barrier per stage publishes
-// stage k and retires the buffer that stage k+1 is then loaded into.  Inside a stage the
-// fragments of the second 64-byte K half are read while the first half's products run.
+// 128 bytes, whole cache lines) into two stage buffers.  One barrier per stage, in its
+// middle: after stage k's last fragment read it publishes stage k+1 and retires stage k's
+// buffer, which then takes stage k+2; the half-0 fragments of stage k+1 are read while
+// stage k's second half of products runs.
 // Each 128-byte row holds 8 chunks of 16 bytes stored at chunk ^ lds_swz(row), which
 // makes the ds_read_b128 fragment reads bank-conflict free.
 //
@@ -125,21 +126,18 @@ __device__ __forceinline__ void zero_tail(uint8_t* stage, int valid_chunks) {
   }
 }
 
+// One K stage of a wave's products in two halves (64 bytes of K each) around the stage's
+// barrier.  Half 0 runs on A / B fragments read before it; after its products come the
+// reads of half 1's fragments (each A fragment's registers take its half-1 fragment once
+// its products have issued), so that every read of the stage is issued before the barrier.
 template <class C>
-__device__ __forceinline__ void mma_stage(const uint8_t* stage, int wrow0, int xrow0, int lane,
-                                          v16f (&acc)[C::TN][C::TM]) {
+__device__ __forceinline__ void mma_half0(const uint8_t* stage, int wrow0, int xrow0, int lane, v8i (&af)[C::TN],
+                                          const v8i (&bf)[C::TM], v8i (&bf1)[C::TM], v16f (&acc)[C::TN][C::TM]) {
   const uint8_t* tW = stage;
   const uint8_t* tX = stage + C::BN * GEMM_BK;
-  const int r = lane & 31, c0 = 2 * (lane >> 5), c1 = 4 + c0;
-  v8i af[C::TN], bf[C::TM], bf1[C::TM];
-#pragma unroll
-  for (int t = 0; t < C::TN; ++t) af[t] = lds_frag(tW, wrow0 + 32 * t + r, c0);
-#pragma unroll
-  for (int t = 0; t < C::TM; ++t) bf[t] = lds_frag(tX, xrow0 + 32 * t + r, c0);
+  const int r = lane & 31, c1 = 4 + 2 * (lane >> 5);
 #pragma unroll
   for (int t = 0; t < C::TM; ++t) bf1[t] = lds_frag(tX, xrow0 + 32 * t + r, c1);
-  // first K half; each A fragment's registers take its second-half fragment once its
-  // products have issued
 #pragma unroll
   for (int a = 0; a < C::TN; ++a) {
 #pragma unroll
@@ -148,11 +146,25 @@ __device__ __forceinline__ void mma_stage(const uint8_t* stage, int wrow0, int x
     af[a] = lds_frag(tW, wrow0 + 32 * a + r, c1);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// Half 1 of a stage (after its barrier).  The half-0 fragments of the following stage
+// (`next`, landed) are read while these products run: B first (free since half 0), then
+// each A fragment once its products have issued.
+template <class C>
+__device__ __forceinline__ void mma_half1(const uint8_t* next, int wrow0, int xrow0, int lane, v8i (&af)[C::TN],
+                                          v8i (&bf)[C::TM], const v8i (&bf1)[C::TM], v16f (&acc)[C::TN][C::TM]) {
+  const int r = lane & 31, c0 = 2 * (lane >> 5);
 #pragma unroll
-  for (int a = 0; a < C::TN; ++a)
+  for (int t = 0; t < C::TM; ++t) bf[t] = lds_frag(next + C::BN * GEMM_BK, xrow0 + 32 * t + r, c0);
+#pragma unroll
+  for (int a = 0; a < C::TN; ++a) {
 #pragma unroll
     for (int b = 0; b < C::TM; ++b)
       acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[a], bf1[b], acc[a][b], 0, 0, 0, 0, 0, 0);
+    af[a] = lds_frag(next, wrow0 + 32 * a + r, c0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 __device__ __forceinline__ v8bf lds_chunk_bf16(const uint8_t* tile, int row, int chunk) {
@@ -274,32 +286,73 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
-    // nk >= 1 (K >= 16): a do-while tells the compiler that the wait below runs before the
+    // Barrier in the middle of each stage, after its last LDS read: the next stage has
+    // landed everywhere (each wave waited for its share of the copy, issued one barrier
+    // earlier) and this stage's buffer is free for the copy two stages ahead.  The next
+    // stage's half-0 fragments are then read while this stage's half-1 products run, and
+    // the barrier's wait overlaps the half-0 products in flight, so the matrix cores do not
+    // stall on a fragment read after every barrier (a barrier at the top of each stage,
+    // before its first reads, measured 2-5% slower; products and their order per
+    // accumulator are the same).  The stage after the tile's last is the next tile's first
+    // (or, with LoRA chunks in LDS, chunk 0), copied into the buffer the next tile's
+    // mainloop starts on.  With a K tail, the last stage's missing chunks are zeroed after
+    // it lands and before its first read.
+    // Entering: stage 0 of this tile is the only copy in flight, into buffer gs & 1 (the
+    // epilogue operands, older, aside).
+    auto after_last = [&](uint8_t* dst) {
+      if constexpr (LM == LORA_LDS) {
+        lora_dma(dst, tm, tn, 0);
+      } else {
+        if (s_next < ntiles) {
+          wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
+          xrs = rsrc(a8, tm_n * C::BM, M, C::BM);
+          gemm_dma<C>(wrs, xrs, dst, lane_off, K, wave, 0);
+        }
+      }
+    };
+    wait_vm0();
+    block_barrier();
+    if (KTAIL && nk == 1) {
+      zero_tail<C>(smem + (gs & 1) * C::STAGE, (K % GEMM_BK) >> 4);
+      block_barrier();
+    }
+    if (nk > 1)
+      gemm_dma<C>(wrs, xrs, smem + ((gs + 1) & 1) * C::STAGE, lane_off, K, wave, GEMM_BK);
+    else
+      after_last(smem + ((gs + 1) & 1) * C::STAGE);
+    v8i af[TN], bf[TM], bf1[TM];
+    {
+      const uint8_t* cur = smem + (gs & 1) * C::STAGE;
+      const int r = lane & 31, c0 = 2 * (lane >> 5);
+#pragma unroll
+      for (int a = 0; a < TN; ++a) af[a] = lds_frag(cur, wrow0 + 32 * a + r, c0);
+#pragma unroll
+      for (int b = 0; b < TM; ++b) bf[b] = lds_frag(cur + C::BN * GEMM_BK, xrow0 + 32 * b + r, c0);
+    }
+    // nk >= 1 (K >= 16): a do-while tells the compiler that the waits inside run before the
     // epilogue, which then waits for none of the loads issued before the mainloop (a wait
     // there would also wait for the next tile's first stage, in flight by then).
     int ks = 0;
     do {
       uint8_t* cur = smem + (gs & 1) * C::STAGE;
       uint8_t* nxt = smem + ((gs + 1) & 1) * C::STAGE;
-      // Stage gs is this wave's only DMA in flight (and the epilogue operands, older).
-      // After the barrier every wave's copy of it has landed and every wave has finished
-      // stage gs-1, whose buffer then takes stage gs+1 while stage gs is multiplied.
-      wait_vm0();
-      block_barrier();
-      if (KTAIL && ks == nk - 1) {
-        zero_tail<C>(cur, (K % GEMM_BK) >> 4);
-        block_barrier();
-      }
+      mma_half0<C>(cur, wrow0, xrow0, lane, af, bf, bf1, acc);
       if (ks + 1 < nk) {
-        gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, (ks + 1) * GEMM_BK);
-      } else if (LM == LORA_LDS) {
-        lora_dma(nxt, tm, tn, 0);
-      } else if (s_next < ntiles) {
-        wrs = rsrc(w8, tn_n * C::BN, N, C::BN);
-        xrs = rsrc(a8, tm_n * C::BM, M, C::BM);
-        gemm_dma<C>(wrs, xrs, nxt, lane_off, K, wave, 0);
+        wait_vm0();
+        block_barrier();
+        if (KTAIL && ks + 2 == nk) {
+          zero_tail<C>(nxt, (K % GEMM_BK) >> 4);
+          block_barrier();
+        }
+        if (ks + 2 < nk)
+          gemm_dma<C>(wrs, xrs, cur, lane_off, K, wave, (ks + 2) * GEMM_BK);
+        else
+          after_last(cur);
       }
-      mma_stage<C>(cur, wrow0, xrow0, lane, acc);
+      // (after the last stage the reads of `nxt` fetch nothing that is used: the next tile
+      // reads its first fragments after its first barrier; one code path keeps the
+      // accumulators in place)
+      mma_half1<C>(nxt, wrow0, xrow0, lane, af, bf, bf1, acc);
       ++gs;
     } while (++ks < nk);
 

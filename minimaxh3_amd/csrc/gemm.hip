@@ -679,10 +679,11 @@ static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, c
   int grid = device_cus() * per_cu;
   grid = grid >= 8 ? grid & ~7 : ntiles;
   if (grid <= 0 || grid > ntiles) grid = ntiles;
-  // Token-tiles per L2 group (measured on MI355X at M = 20280): long-K products (each
-  // panel 3 MB at K = 12288) share best in groups of 2, the K = 3072 ones in groups of 8
-  // (QKV: 8 < 16 < 32; MLP-up: 8 about 1% ahead of 4 and 16).
-  const int group_m = K >= 8192 ? 2 : 8;
+  // Token-tiles per L2 group (measured on MI355X at M = 20280, one process): long-K products
+  // (each panel 3 MB at K = 12288) share best in groups of 4 (MLP-down 584-586 us against 592
+  // with 2 and 602 with 1), the K = 3072 ones in groups of 8 (out-projection and MLP-up 1-2%
+  // ahead of 4 and 16; QKV within 1.5% from 4 to 16).
+  const int group_m = K >= 8192 ? 4 : 8;
   gemm_fp8_rowwise_kernel<C, ACT, LM, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
       a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n, group_m);
 }

@@ -66,6 +66,15 @@ __device__ __forceinline__ void wait_vm0() {
   asm volatile("" ::: "memory");
 }
 
+// s_waitcnt vmcnt(N) the same way: at most N of this wave's vector memory operations still
+// in flight (they complete in issue order).  vmcnt is 6 bits: bits 3:0 and 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+  asm volatile("" ::: "memory");
+}
+
 // Two fp32 values -> two 16-bit values (ODT = MXF8_BF16 / MXF8_F16), a in the low half, in
 // one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: round to nearest even, the same bits as
 // f32_to_bf16_bits / f32_to_f16_bits for every non-NaN input (NaN stays NaN).

@@ -571,26 +571,43 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
 }
 
 // ---- LoRA down-projection t = bf16(x A^T): x [M,K] bf16, A [r,K] bf16 -> t [M,r] -----
-// A workgroup computes 128 rows of t by up to 128 rank columns (blockIdx.y selects columns
-// [128 y, 128 y + 128)) on 4 waves of 32 rows, RT accumulators of 32 columns each.  K is
-// consumed 64 elements (128 bytes per row) per stage: the x tile (128 rows) and the A tile
-// (32 RT rows) are copied global -> LDS with the DMA into two stage buffers in the GEMM's
-// row layout, so the four waves share one copy of A.  K step j of a stage reads logical
-// chunk 2j + g of both operands (a consistent K permutation).
-constexpr int LD_BM = 128;
+// A workgroup computes BM = 32 W rows of t by up to 128 rank columns (blockIdx.y selects
+// columns [128 y, 128 y + 128)) on W waves of 32 rows, RT accumulators of 32 columns each.
+// K is consumed 64 elements (128 bytes per row) per stage: the x tile (BM rows) and the A
+// tile (32 RT rows) are copied global -> LDS with the DMA in the GEMM's row layout, so the
+// waves share one copy of A.  K step j of a stage reads logical chunk 2j + g of both
+// operands (a consistent K permutation); a 32-row block's products and their order do not
+// depend on W, so neither do the results.
+// The pass is bound by how many bytes of x are in flight (the products are a few percent of
+// the time): the stages form a ring as deep as one CU's 160 KB of LDS holds (one workgroup
+// per CU), and the copy of stage ks + NS - 1 is issued while stage ks is consumed.  The
+// host picks W so that the tiles come out in whole rounds over the CUs.
+constexpr int LD_BM_MAX = 160;
+template <int RT, int W>
+struct LoraDown {
+  static constexpr int BM = 32 * W, AR = 32 * RT, STAGE = (BM + AR) * GEMM_BK;
+  // DMA instructions per wave and stage: 4 of x (8 rows each) and the A tile's 4 RT dealt
+  // round-robin (waves below A_EXTRA take one more)
+  static constexpr int A_LO = (4 * RT) / W, A_EXTRA = (4 * RT) % W;
+  static constexpr int P_LO = 4 + A_LO, P_HI = P_LO + (A_EXTRA ? 1 : 0);
+  static constexpr int NS_LDS = (160 * 1024) / STAGE, NS_CNT = 2 + 63 / P_HI;
+  static constexpr int NS = NS_LDS < NS_CNT ? (NS_LDS < 8 ? NS_LDS : 8) : (NS_CNT < 8 ? NS_CNT : 8);
+  static_assert(NS >= 3 && (NS - 2) * P_HI < 64, "ring depth");
+};
 
-template <int RT>
-__global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restrict__ x, int ldxb,
-                                                        const uint8_t* __restrict__ a, uint16_t* __restrict__ t, int M,
-                                                        int K, int r) {
-  constexpr int AR = 32 * RT, STAGE = (LD_BM + AR) * GEMM_BK;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+template <int RT, int W>
+__global__ __launch_bounds__(64 * W) void lora_down_kernel(const uint8_t* __restrict__ x, int ldxb,
+                                                           const uint8_t* __restrict__ a, uint16_t* __restrict__ t,
+                                                           int M, int K, int r) {
+  using L = LoraDown<RT, W>;
+  constexpr int BM = L::BM, AR = L::AR, STAGE = L::STAGE, NS = L::NS;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int m0 = blockIdx.x * LD_BM, j0 = blockIdx.y * 128;
+  const int m0 = blockIdx.x * BM, j0 = blockIdx.y * 128;
   const int Kb = 2 * K;
   const int nk = (K + 63) / 64;
   const __amdgpu_buffer_rsrc_t xrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(x + (int64_t)m0 * ldxb), 0, min(M - m0, LD_BM) * ldxb, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + (int64_t)m0 * ldxb), 0, min(M - m0, BM) * ldxb, 0x00020000);
   const __amdgpu_buffer_rsrc_t ars =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a + (int64_t)j0 * Kb), 0, min(r - j0, AR) * Kb, 0x00020000);
   // lane i of a DMA instruction J fills tile row 8J + i/8, physical chunk i%8 = logical
@@ -604,16 +621,17 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restric
   }
   auto dma = [&](uint8_t* st, int kb0) {
 #pragma unroll
-    for (int j = 0; j < LD_BM / 32; ++j) {
-      const int J = (LD_BM / 32) * wave + j;
+    for (int j = 0; j < 4; ++j) {
+      const int J = 4 * wave + j;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, LDS_PTR(st + J * 1024), 16, xoff[J & 1], 8 * J * ldxb + kb0, 0,
                                                0);
     }
 #pragma unroll
-    for (int j = 0; j < RT; ++j) {
-      const int J = RT * wave + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, LDS_PTR(st + LD_BM * GEMM_BK + J * 1024), 16, aoff[J & 1],
-                                               8 * J * Kb + kb0, 0, 0);
+    for (int j = 0; j < L::A_LO + (L::A_EXTRA ? 1 : 0); ++j) {
+      const int J = wave + W * j;
+      if (j < L::A_LO || wave < L::A_EXTRA)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, LDS_PTR(st + BM * GEMM_BK + J * 1024), 16, aoff[J & 1],
+                                                 8 * J * Kb + kb0, 0, 0);
     }
   };
   v16f acc[RT];
@@ -622,25 +640,36 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint8_t* __restric
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[u][i] = 0.0f;
   const int g = lane >> 5, xr = 32 * wave + (lane & 31);
-  dma(smem, 0);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) dma(smem + s * STAGE, s * GEMM_BK);
+  int slot = 0;  // ks % NS
   for (int ks = 0; ks < nk; ++ks) {
-    uint8_t* cur = smem + (ks & 1) * STAGE;
-    // stage ks is this wave's only DMA in flight; after the barrier every wave's copy of
-    // it has landed and every wave has finished stage ks - 1, whose buffer takes ks + 1
-    wait_vm0();
+    uint8_t* cur = smem + slot * STAGE;
+    // this wave's copies in flight are stages ks .. min(ks + NS - 2, nk - 1), P_LO or P_HI
+    // instructions each and nothing else; wait for stage ks (for all of them near the end).
+    // After the barrier every wave's copy of stage ks has landed and every wave has finished
+    // stage ks - 1, whose slot takes stage ks + NS - 1.
+    if (ks + NS - 2 >= nk)
+      wait_vm0();
+    else if (L::A_EXTRA && wave < L::A_EXTRA)
+      wait_vm<(NS - 2) * L::P_HI>();
+    else
+      wait_vm<(NS - 2) * L::P_LO>();
     block_barrier();
     if (ks == nk - 1 && (K & 63)) {
       // zero the chunks at or past K (they hold the next row's elements)
       const int valid = (K & 63) >> 3;
-      for (int e = threadIdx.x; e < (LD_BM + AR) * 8; e += 256) {
-        const int row = e >> 3, c = e & 7, trow = row < LD_BM ? row : row - LD_BM;
+      for (int e = threadIdx.x; e < (BM + AR) * 8; e += 64 * W) {
+        const int row = e >> 3, c = e & 7, trow = row < BM ? row : row - BM;
         if (c >= valid)
           *reinterpret_cast<v4i*>(cur + row * GEMM_BK + ((c ^ lds_swz<GEMM_BK>(trow)) << 4)) = v4i{0, 0, 0, 0};
       }
       block_barrier();
     }
-    if (ks + 1 < nk) dma(smem + ((ks + 1) & 1) * STAGE, (ks + 1) * GEMM_BK);
-    const uint8_t* tA = cur + LD_BM * GEMM_BK;
+    if (ks + NS - 1 < nk) dma(smem + (slot == 0 ? NS - 1 : slot - 1) * STAGE, (ks + NS - 1) * GEMM_BK);
+    slot = slot + 1 == NS ? 0 : slot + 1;
+    const uint8_t* tA = cur + BM * GEMM_BK;
 #pragma unroll
     for (int j = 0; j < GEMM_BK / 32; ++j) {
       const v8bf xf = lds_chunk_bf16(cur, xr, 2 * j + g);
@@ -763,22 +792,40 @@ extern "C" int mxf8_lora_down(const void* x, int64_t ldx, const void* a, void* t
   if (r % 16 || r > 4096) return set_error(MXF8_EINVAL, "lora_down: r must be a multiple of 16 and <= 4096");
   if (K % 8 || ldx % 8 || ldx < K || ((uintptr_t)x % 16) || ((uintptr_t)a % 16) || ((uintptr_t)t % 8))
     return set_error(MXF8_EINVAL, "lora_down: K, ldx must be multiples of 8 (ldx >= K) and operands aligned");
-  // per-workgroup buffer ranges are 128 rows of x and 128 rows of A
-  if (M > 0x7fffffff / 2 || ldx > 0x7fffffff / (2 * LD_BM) || K > 0x7fffffff / (2 * 128))
+  // per-workgroup buffer ranges are up to 160 rows of x and 128 rows of A
+  if (M > 0x7fffffff / 2 || ldx > 0x7fffffff / (2 * LD_BM_MAX) || K > 0x7fffffff / (2 * 128))
     return set_error(MXF8_EINVAL, "lora_down: shape too large");
-  const dim3 grid((unsigned)cdiv(M, LD_BM), (unsigned)cdiv(r, 128));
+  const int64_t col_blocks = cdiv(r, 128);
+  // Rows per workgroup (32 W): with one workgroup per CU the busiest CU handles
+  // ceil(tiles / CUs) tiles, so take the W with the fewest rows on it (ties: the larger
+  // tile, fewer copies of A).  M = 77648 on 256 CUs: 160 rows, 486 tiles in 2 rounds,
+  // against 607 tiles of 128 rows in 3.
+  const int64_t cus = device_cus();
+  int W = 5;
+  int64_t best = INT64_MAX;
+  for (int w = 5; w >= 2; --w) {
+    const int64_t rows = cdiv(cdiv(M, 32 * w) * col_blocks, cus) * 32 * w;
+    if (rows < best) best = rows, W = w;
+  }
+  const dim3 grid((unsigned)cdiv(M, 32 * W), (unsigned)col_blocks);
   const uint8_t* xb = static_cast<const uint8_t*>(x);
   const uint8_t* ab = static_cast<const uint8_t*>(a);
   uint16_t* t16 = static_cast<uint16_t*>(t);
   const int rs = (int)(r < 128 ? r : 128);  // rank columns per workgroup
+  const int RT = (rs + 31) / 32;
   const int ldxb = (int)(2 * ldx);
-  if (rs <= 32)
-    lora_down_kernel<1><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
-  else if (rs <= 64)
-    lora_down_kernel<2><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
-  else if (rs <= 96)
-    lora_down_kernel<3><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
-  else
-    lora_down_kernel<4><<<grid, 256, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r);
-  return check_launch("lora_down");
+#define MXF8_LORA_DOWN_CASE(rt, w)                                                                  \
+  if (RT == rt && W == w) {                                                                         \
+    lora_down_kernel<rt, w><<<grid, 64 * w, 0, stream>>>(xb, ldxb, ab, t16, (int)M, (int)K, (int)r); \
+    return check_launch("lora_down");                                                               \
+  }
+#define MXF8_LORA_DOWN_CASES(rt) \
+  MXF8_LORA_DOWN_CASE(rt, 2) MXF8_LORA_DOWN_CASE(rt, 3) MXF8_LORA_DOWN_CASE(rt, 4) MXF8_LORA_DOWN_CASE(rt, 5)
+  MXF8_LORA_DOWN_CASES(1)
+  MXF8_LORA_DOWN_CASES(2)
+  MXF8_LORA_DOWN_CASES(3)
+  MXF8_LORA_DOWN_CASES(4)
+#undef MXF8_LORA_DOWN_CASES
+#undef MXF8_LORA_DOWN_CASE
+  return set_error(MXF8_EINVAL, "lora_down: no kernel for %d rank tiles, %d waves", RT, W);
 }

@@ -295,6 +295,28 @@ def test_lora_down_matches_bf16_matmul():
         np.testing.assert_allclose(t, ref, rtol=2 ** -7, atol=1e-3 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("r", [64, 96])
+def test_lora_down_rows_independent_of_tile_height(r):
+    """lora_down picks the rows per workgroup (64, 96, 128 or 160) from M and the CU count, so
+    that the tiles fill whole rounds; a row's result must not depend on that choice.  Prefixes of
+    one x (77648 rows: the 720p token count, 20280, 32768, 5000, 300) give the same rows bit for
+    bit, and sampled rows of the full call match the float64 product rounded to bf16."""
+    _say(f"lora_down tile heights r={r}")
+    from minimaxh3_amd import ops
+    torch.manual_seed(11)
+    M, K = 77648, 264  # K % 64 != 0: the zeroed tail chunks take part too
+    x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+    A = (torch.randn((r, K), device="cuda") * 0.05).to(torch.bfloat16)
+    full = ops.lora_down(x, A)
+    for m in (32768, 20280, 5000, 300):
+        assert torch.equal(ops.lora_down(x[:m], A).view(torch.int16), full[:m].view(torch.int16)), m
+    rows = torch.randint(0, M, (512,), generator=torch.Generator().manual_seed(1)).cuda()
+    dot = x[rows].double() @ A.double().t()
+    ref = dot.float().to(torch.bfloat16).float()
+    got = full[rows].float()
+    torch.testing.assert_close(got, ref, rtol=2 ** -7, atol=1e-3 * ref.abs().max().item())
+
+
 @pytest.mark.parametrize("rank", [0, 64, 128])
 def test_forward_adaln_equals_forward_of_modulation(fl, rank):
     """FP8Linear.forward_adaln(x, shift, scale) == FP8Linear.forward(y) bit for bit, with no

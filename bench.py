@@ -335,7 +335,7 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
     act_grid = str(math.ceil(tokens / 4) * 256)
     out, k = {}, 0
     na = len(attn_names)
-    ka = kq = 0  # attention launches and K/V quantizer folds so far (a step runs them in order)
+    ka = kq = kl = 0  # attention, K/V quantizer and LoRA-down launches so far (in step order)
 
     def sfx(i):
         return "" if na == 1 else f"[{attn_names[i % na]}]"
@@ -351,8 +351,9 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
             out[d] = "quant_rows<0, 24>[mlp_down]" if "<0, 24" in name else "quant_rows<0, 6>"
         elif "adaln_quant_rows_kernel" in name:
             out[d] = "adaln_quant_rows"
-        elif "lora_down_kernel" in name:
-            out[d] = "lora_down"
+        elif "lora_down_kernel" in name:  # every linear of a LoRA workload runs one, in LINEARS order
+            out[d] = f"lora_down[{LINEARS[kl % len(LINEARS)][0]}]"
+            kl += 1
         elif "attn_fwd_kernel" in name or "attn_fwd_resident_kernel" in name:
             out[d] = "attn_fwd" + sfx(ka)
             ka += 1
@@ -369,7 +370,8 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
 
 
 PART_ORDER = ("gemm[qkv]", "gemm[attn_out]", "gemm[mlp_up]", "gemm[mlp_down]", "quant_rows<0, 6>",
-              "quant_rows<0, 24>[mlp_down]", "adaln_quant_rows", "lora_down", "attn_quant_kv: colreduce", "attn_quant_kv: fold",
+              "quant_rows<0, 24>[mlp_down]", "adaln_quant_rows", "lora_down[qkv]", "lora_down[attn_out]",
+              "lora_down[mlp_up]", "lora_down[mlp_down]", "attn_quant_kv: colreduce", "attn_quant_kv: fold",
               "attn_quant_kv: quantize", "attn_fwd", "torch.neg 1 GiB (HBM reference)")
 
 

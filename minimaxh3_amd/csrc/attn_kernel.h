@@ -787,19 +787,23 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
   // the loop's first barrier) cannot reach before every wave has read it.
   if constexpr (QF) cx.template quant_q<ODT>(qa, Sq, nq, reinterpret_cast<float*>(smem + T::BUF));
   int j = j0;
-  for (int i = 0; i < nk; ++i) {
+  // Tile i uses buffer i & 1.  The loop takes the tiles in pairs so that each buffer's
+  // address is a constant: the LDS fragment reads then carry it in their immediate offset
+  // instead of adding it to every lane offset on every tile.
+  auto tile = [&](auto par, int i) {
+    constexpr int PAR = decltype(par)::value;
     // Tile i is the only DMA in flight; after the barrier every wave has finished tile
     // i-1, so its buffer can take tile i+1 while tile i is computed.
     wait_vm0();
     attn_barrier();
     const int jn = j + 1 == nk ? 0 : j + 1;
     if (i + 1 < nk) {
-      uint8_t* nb = smem + ((i + 1) & 1) * T::BUF;
+      uint8_t* nb = smem + (1 - PAR) * T::BUF;
       cx.dma_k(nb, jn * 128);
       cx.dma_v(nb + T::KB, jn * 128);
       cx.dma_aux(nb + T::KB + T::VB, jn * 128, Sk);
     }
-    const uint8_t* buf = smem + (i & 1) * T::BUF;
+    const uint8_t* buf = smem + PAR * T::BUF;
     const float skj = cx.skh[j];
     const int kv0 = j * 128;
     v16f s[4];
@@ -812,6 +816,10 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     st.m = m_new;
     AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
+  };
+  for (int i = 0; i < nk; i += 2) {
+    tile(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < nk) tile(std::integral_constant<int, 1>{}, i + 1);
   }
   AttnSv<D> svr;
   svr.load(sv, cx.bh, lane);

@@ -309,6 +309,14 @@ struct AttnState {
   // (see AttnMfmaRun, x == NDT).
   v4f lacc;
   float m;  // lazy row max (log2 domain)
+  // the code constants that depend on m (see attn_codes_w4): 56 - 8 m and (48 - 8 m) 2^64
+  float cst, cstf;
+
+  __device__ __forceinline__ void set_m(float m_new) {
+    m = m_new;
+    cst = 56.0f - 8.0f * m_new;
+    cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
+  }
 
   __device__ __forceinline__ void init() {
 #pragma unroll
@@ -317,7 +325,7 @@ struct AttnState {
       for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) lacc[i] = 0.0f;
-    m = kAttnNeg;
+    set_m(kAttnNeg);
   }
 
   // O, l *= alpha (a moved lazy max)
@@ -390,13 +398,14 @@ struct AttnPB {
 // Per-tile constants of the code arithmetic (see attn_codes_w4).
 struct AttnCodeK {
   float c8, cst, c8f, cstf, tau;
+  // cst = 56 - 8 m_new and cstf = (48 - 8 m_new) 2^64 come with the row max (AttnState)
   template <bool HAS_BIAS>
-  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float m_new, float tau) {
+  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float cst, float cstf, float tau) {
     AttnCodeK k;
-    k.cst = 56.0f - 8.0f * m_new;
+    k.cst = cst;
     k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
     k.c8f = k.c8 * 0x1p64f;
-    k.cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
+    k.cstf = cstf;
     k.tau = tau;
     return k;
   }
@@ -656,29 +665,39 @@ __device__ __forceinline__ float attn_part_max(const v16f (&s)[4], float sq, flo
     for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], s[t][i]);
   float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
   {
-    // partner lane^32 through v_permlane32_swap (two copies: each half receives the other)
+    // partner lane^32 through v_permlane32_swap (two copies: each half receives the other).
+    // Both are dot products of finite e4m3 codes, hence finite, so a plain v_max_f32 is
+    // fmaxf; written out, because the compiler would first canonicalize both operands.
     const uint32_t u = __float_as_uint(mx);
     const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    asm("v_max_f32 %0, %1, %2" : "=v"(mx) : "v"(__uint_as_float(sw[0])), "v"(__uint_as_float(sw[1])));
   }
   return fmaxf(HAS_BIAS ? mx : (mx * sq) * skj, kAttnNeg);
 }
 
 // The lazy-max decision (kernels/fp8_attention.py:264): the row max moves to the tile's
-// maximum rmax only when that exceeds it by more than 8, or while it is still -1e9.
-__device__ __forceinline__ float attn_lazy_max(float rmax, float m_old) {
-  return (rmax > m_old + 8.0f || m_old == kAttnNeg) ? rmax : m_old;
-}
+// maximum rmax only when that exceeds it by more than 8, or while it is still -1e9.  The
+// second test changes nothing here: rmax >= -1e9 (attn_part_max clamps it) and -1e9 + 8
+// rounds to -1e9 in fp32 (its ulp is 64), so with m_old = -1e9 either rmax > m_old + 8 or
+// rmax = -1e9 = m_old, and both branches give rmax.  Returns whether the max moves.
+__device__ __forceinline__ bool attn_max_moves(float rmax, float m_old) { return rmax > m_old + 8.0f; }
 
-// Row max, lazy-max decision and the codes of the whole tile; returns m_new.
-template <bool HAS_BIAS, bool REP>
-__device__ __forceinline__ float attn_codes(const v16f (&s)[4], float sq, float skj, float m_old, float tau,
-                                            AttnPB<REP>& pb) {
-  const float m_new = attn_lazy_max(attn_part_max<HAS_BIAS>(s, sq, skj), m_old);
-  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, m_new, tau);
+// One tile's row max and lazy-max decision, the rescale of O and l when the max moves
+// (rescale = false: they are still zero, and scaling them would change no bit), and the
+// tile's codes.  Rows whose max stays take alpha = 1 in a rescale, which changes no bit.
+template <bool HAS_BIAS, bool REP, int D>
+__device__ __forceinline__ void attn_softmax_tile(const v16f (&s)[4], float sq, float skj, float tau, bool rescale,
+                                                  AttnState<D>& st, AttnPB<REP>& pb) {
+  const float rmax = attn_part_max<HAS_BIAS>(s, sq, skj);
+  const bool moves = attn_max_moves(rmax, st.m);
+  if (__builtin_amdgcn_ballot_w64(moves)) {
+    const float m_new = moves ? rmax : st.m;
+    if (rescale) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
+    st.set_m(m_new);
+  }
+  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, st.cst, st.cstf, tau);
 #pragma unroll
   for (int t = 0; t < 4; ++t) attn_codes_sub<REP>(s[t], k, t, pb);
-  return m_new;
 }
 
 // The channel scales sv of head bh that this lane's output channels take (see attn_store).
@@ -811,9 +830,7 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-    const float m_new = attn_codes<HAS_BIAS, DO_REPAIR>(s, cx.sqI, skj, st.m, tau, pb);
-    if (__builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
-    st.m = m_new;
+    attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, tau, true, st, pb);
     AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
   };
@@ -960,10 +977,8 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-        const float m_new = attn_codes<HAS_BIAS, false>(s, cx.sqI, skj, st.m, -1.0f, pb);
         // O and l are still zero on the first tile: rescaling them changes no bit
-        if (i > 0 && __builtin_amdgcn_ballot_w64(m_new != st.m)) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
-        st.m = m_new;
+        attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, -1.0f, i > 0, st, pb);
         AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         j = j + 1 == nk ? 0 : j + 1;
       }

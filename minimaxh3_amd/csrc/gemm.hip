@@ -70,6 +70,13 @@ __device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
 __device__ __forceinline__ uint32_t bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
 }
+// bf16r of two values with one conversion: the low half moves up, the high half is masked
+// (three instructions for two roundings instead of four)
+__device__ __forceinline__ void bf16r2(float& a, float& b) {
+  const uint32_t w = bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
 
 // 16 bytes of an output tile.  Whole tiles leave with non-temporal stores: the kernel never
 // reads them back, and streaming the lines out of the L2 early leaves it to the operand panels
@@ -431,18 +438,29 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     // Output values of accumulators x (registers 4 q .. 4 q + 3 of a block, whose LoRA
     // branch is lacc), packed as two bf16 pairs.
     auto out_quad = [&](const v4f x, int q, const v16f& lacc, float sam, const v4f& swq, const v4f& bq) {
+      // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch * scale,
+      // bf16 sum; GELU-tanh acts on the bf16 result.  Values go through them in pairs
+      // (bf16r2); the last rounding is the output packing itself.
       float v[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = __builtin_fmaf(x[e] * sam, swq[e], bq[e]);
-        // the reference's roundings: bf16 linear output, bf16 branch, bf16 branch * scale,
-        // bf16 sum; GELU-tanh acts on the bf16 result
-        if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) v[e] = bf16r(v[e]);
+      for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(x[e] * sam, swq[e], bq[e]);
+#pragma unroll
+      for (int h = 0; h < 4; h += 2) {
+        if constexpr (LM != LORA_NONE || ACT == MXF8_ACT_GELU_TANH) bf16r2(v[h], v[h + 1]);
         if constexpr (LM != LORA_NONE) {
-          const float br = bf16r(bf16r(lacc[4 * q + e]) * lora_scale);
-          v[e] = bf16r(v[e] + br);
+          float b0 = lacc[4 * q + h], b1 = lacc[4 * q + h + 1];
+          bf16r2(b0, b1);
+          b0 *= lora_scale;
+          b1 *= lora_scale;
+          bf16r2(b0, b1);
+          v[h] += b0;
+          v[h + 1] += b1;
+          if constexpr (ACT == MXF8_ACT_GELU_TANH) bf16r2(v[h], v[h + 1]);
         }
-        if constexpr (ACT == MXF8_ACT_GELU_TANH) v[e] = gelu_tanh_f32(v[e]);
+        if constexpr (ACT == MXF8_ACT_GELU_TANH) {
+          v[h] = gelu_tanh_f32(v[h]);
+          v[h + 1] = gelu_tanh_f32(v[h + 1]);
+        }
       }
       return make_uint2(bf16x2(v[0], v[1]), bf16x2(v[2], v[3]));
     };

@@ -450,9 +450,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
         if constexpr (LM != LORA_NONE) {
           float b0 = lacc[4 * q + h], b1 = lacc[4 * q + h + 1];
           bf16r2(b0, b1);
-          b0 *= lora_scale;
-          b1 *= lora_scale;
-          bf16r2(b0, b1);
+          // scale 1 (the runtime folds alpha / rank into B): bf16(b * 1) = b, so the product
+          // and its rounding change no bit and are skipped
+          if (lora_scale != 1.0f) {
+            b0 *= lora_scale;
+            b1 *= lora_scale;
+            bf16r2(b0, b1);
+          }
           v[h] += b0;
           v[h + 1] += b1;
           if constexpr (ACT == MXF8_ACT_GELU_TANH) bf16r2(v[h], v[h + 1]);

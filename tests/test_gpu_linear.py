@@ -373,6 +373,32 @@ def test_gemm_lora_epilogue_matches_oracle(M, N, K, r, gelu):
     assert np.abs(ref - no_lora).max() > 5e-2 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("M,N,K,r,gelu", [
+    (600, 3072, 3072, 64, False),   # LoRA operands in LDS, 256 x 256 tiles
+    (600, 3072, 3072, 64, True),
+    (300, 512, 256, 192, False),    # read from global memory in the epilogue
+])
+def test_gemm_lora_scale_one_equals_scaled_branch(M, N, K, r, gelu):
+    """Scale 1 (what the runtime passes: alpha / rank is folded into B) skips the branch's
+    product and second rounding.  Scaling by powers of two commutes with every bf16 rounding
+    of the branch (normal range), so (B, scale 1) and (2 B, scale 0.5) must give the same
+    bits: the skipped path against the full one."""
+    _say(f"gemm lora scale one M={M} N={N} K={K} r={r} gelu={gelu}")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(7 + r)
+    x = to_gpu(with_outliers(rng, bf16_randn(rng, (M, K))))
+    w8, sw = ops.quant_rows(to_gpu(bf16_randn(rng, (N, K), 0.02)))
+    b = to_gpu(bf16_randn(rng, (N,), 0.01))
+    A, B = to_gpu(bf16_randn(rng, (r, K), 0.08)), to_gpu(bf16_randn(rng, (N, r), 0.08))
+    x8, sa = ops.quant_rows(x)
+    lt = ops.lora_down(x, A)
+    one = ops.gemm_rowwise(x8, w8, sa, sw.view(1, -1), b, int(gelu), lt, B, 1.0)
+    half = ops.gemm_rowwise(x8, w8, sa, sw.view(1, -1), b, int(gelu), lt, (B * 2).contiguous(), 0.5)
+    assert torch.equal(one.view(torch.int16), half.view(torch.int16))
+    plain = ops.gemm_rowwise(x8, w8, sa, sw.view(1, -1), b, int(gelu), None, None, 0.0)
+    assert not torch.equal(one.view(torch.int16), plain.view(torch.int16))
+
+
 # ---------------------------------------------------------------- full-size shapes (properties)
 
 @pytest.mark.parametrize("N,K", [(9216, 3072), (12288, 3072), (3072, 12288)])

@@ -270,7 +270,9 @@ __global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* _
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t idx = (int64_t)c * 64 + lane;
-      if (idx < nchunk) reinterpret_cast<uint4*>(y + row * C)[idx] = v[c];
+      if (idx < nchunk)
+        __builtin_nontemporal_store(v4i{(int)v[c].x, (int)v[c].y, (int)v[c].z, (int)v[c].w},
+                                    reinterpret_cast<v4i*>(y + row * C) + idx);
     }
   }
   amax = wave_max(amax);

@@ -666,8 +666,9 @@ __device__ __forceinline__ float attn_part_max(const v16f (&s)[4], float sq, flo
   float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
   {
     // partner lane^32 through v_permlane32_swap (two copies: each half receives the other).
-    // Both are dot products of finite e4m3 codes, hence finite, so a plain v_max_f32 is
-    // fmaxf; written out, because the compiler would first canonicalize both operands.
+    // Both values come from arithmetic, so neither is a signaling NaN, and for those a plain
+    // v_max_f32 is fmaxf (a quiet NaN yields the other operand).  Written out, because the
+    // compiler would first canonicalize both operands, a quieting only signaling NaNs need.
     const uint32_t u = __float_as_uint(mx);
     const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
     asm("v_max_f32 %0, %1, %2" : "=v"(mx) : "v"(__uint_as_float(sw[0])), "v"(__uint_as_float(sw[1])));

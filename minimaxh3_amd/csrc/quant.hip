@@ -270,6 +270,9 @@ __global__ __launch_bounds__(256) void adaln_quant_rows_kernel(const uint16_t* _
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t idx = (int64_t)c * 64 + lane;
+      // non-temporal: at 720p the rows (477 MB) exceed the MALL and the LoRA down-projection
+      // reads them next; streamed out early, they leave it fewer write-backs to wait on (the
+      // pair 329 -> 312 us on MI355X)
       if (idx < nchunk)
         __builtin_nontemporal_store(v4i{(int)v[c].x, (int)v[c].y, (int)v[c].z, (int)v[c].w},
                                     reinterpret_cast<v4i*>(y + row * C) + idx);

@@ -425,15 +425,20 @@ def summarize_counters(directories: list[str]) -> str:
         rows = _csv_rows(d, "counter_collection.csv")
         names = {}
         vals = {}
+        durs = {}
         for r in rows:
             i = int(r["Dispatch_Id"])
             names[i] = (r["Kernel_Name"], r["Grid_Size"])
             vals.setdefault(i, {}).setdefault(r["Counter_Name"], 0.0)
             vals[i][r["Counter_Name"]] += float(r["Counter_Value"])
+            if r["Counter_Name"] == "SQ_BUSY_CYCLES":
+                durs[i] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])  # ns
         lab = _labels([(i, n, g) for i, (n, g) in sorted(names.items())])
         for i, part in lab.items():
             for c, v in vals[i].items():
                 per.setdefault(part, {}).setdefault(c, []).append(v)
+            if i in durs:
+                per.setdefault(part, {}).setdefault("duration_ns", []).append(float(durs[i]))
 
     def m(part, c):
         v = per.get(part, {}).get(c)
@@ -446,9 +451,9 @@ def summarize_counters(directories: list[str]) -> str:
     if fetch_k and write_k:
         lines += [f"Calibration (the 1 GiB bf16 negation reads and writes exactly 1 GiB per launch): bytes read = "
                   f"{fetch_k:.3f} x FETCH_SIZE KiB x 1024, bytes written = {write_k:.3f} x WRITE_SIZE KiB x 1024.", ""]
-    lines += ["| part | kernel cycles (M) | MFMA busy | VALU busy | MFMA+VALU co-issue | LDS busy | wait | "
+    lines += ["| part | kernel cycles (M) | clock GHz | MFMA busy | VALU busy | MFMA+VALU co-issue | LDS busy | wait | "
               "VALU instr / MFMA instr | HBM read MB | HBM write MB |",
-              "|---|---|---|---|---|---|---|---|---|---|"]
+              "|---|---|---|---|---|---|---|---|---|---|---|"]
     for p in PART_ORDER:
         if p not in per:
             continue
@@ -466,14 +471,17 @@ def summarize_counters(directories: list[str]) -> str:
             ratio = f"{m(p, 'SQ_INSTS_VALU') / m(p, 'SQ_INSTS_MFMA'):.1f}"
         rd = f"{m(p, 'FETCH_SIZE') * 1024 * fetch_k / 1e6:.1f}" if m(p, "FETCH_SIZE") is not None and fetch_k else "-"
         wr = f"{m(p, 'WRITE_SIZE') * 1024 * write_k / 1e6:.1f}" if m(p, "WRITE_SIZE") is not None and write_k else "-"
-        lines.append(f"| `{p}` | {cyc / 1e6:.2f} | {frac('SQ_VALU_MFMA_BUSY_CYCLES')} | "
+        dur = m(p, "duration_ns")
+        ghz = f"{cyc / dur:.2f}" if cyc and dur else "-"
+        lines.append(f"| `{p}` | {cyc / 1e6:.2f} | {ghz} | {frac('SQ_VALU_MFMA_BUSY_CYCLES')} | "
                      f"{frac('SQ_ACTIVE_INST_VALU', 4.0)} | {frac('SQ_VALU_MFMA_COEXEC_CYCLES')} | "
                      f"{frac('SQ_ACTIVE_INST_LDS', 4.0)} | {wait} | {ratio} | {rd} | {wr} |"
-                     if cyc else f"| `{p}` | - | - | - | - | - | - | {ratio} | {rd} | {wr} |")
+                     if cyc else f"| `{p}` | - | - | - | - | - | - | - | {ratio} | {rd} | {wr} |")
     lines += ["", "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles); VALU busy = 4 x "
                   "SQ_ACTIVE_INST_VALU (quad-cycles) / the same; co-issue = SQ_VALU_MFMA_COEXEC_CYCLES / the same; "
-                  "LDS busy = 4 x SQ_ACTIVE_INST_LDS / the same; kernel cycles = SQ_BUSY_CYCLES / 32; wait = "
-                  "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."]
+                  "LDS busy = 4 x SQ_ACTIVE_INST_LDS / the same; kernel cycles = SQ_BUSY_CYCLES / 32; clock = "
+                  "kernel cycles / the dispatch's duration in the same pass (the 5.0 PFLOP/s peak assumes 2.4 GHz); "
+                  "wait = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."]
     return "\n".join(lines)
 
 

@@ -84,7 +84,21 @@ WORKLOADS = {
                "of the QKV and MLP-up inputs, 4 FP8 linears (M=77648, hidden 3072, MLP 12288, GELU-tanh on "
                "MLP-up) with a rank-64 LoRA in every epilogue + FP8 flash-attention B=1 H=24 S=77648 D=128",
                77648, 64, (("attn", 1, 77648, 77648, 0),), True),
+    "linear2048": ("FP8 linear x bf16 [2048,3072] ~N(0,1) (no outliers), W [3072,3072] ~N(0,0.02) e4m3 per-channel, "
+                   "bias ~N(0,0.01): per-token activation quantization + row-wise scaled FP8 GEMM, bf16 out",
+                   2048, 0, (), False),
 }
+# the linears of each workload (default: the DiT block's four) and whether 1% of the activation
+# channels are scaled x20
+LINEAR_SETS = {"linear2048": (("linear", HIDDEN, HIDDEN, 0),)}
+NO_OUTLIERS = ("linear2048",)
+# workloads whose step is captured once in a HIP graph and replayed: two launches of ~20 us,
+# which Python launches one by one would not keep the GPU busy with
+GRAPHED = ("linear2048",)
+
+
+def linears_of(workload: str):
+    return LINEAR_SETS.get(workload, LINEARS)
 
 
 def log(msg: str) -> None:
@@ -99,15 +113,17 @@ def attn_flops(b: int, h: int, sq: int, sk: int, d: int) -> float:
     return 4.0 * b * h * sq * sk * d
 
 
-def activations(torch, g, m: int, k: int, dev):
-    """bf16 ~N(0,1) [m, k] with floor(1% of k) channels (seeded randperm) scaled x20."""
+def activations(torch, g, m: int, k: int, dev, outliers: bool = True):
+    """bf16 ~N(0,1) [m, k] with floor(1% of k) channels (seeded randperm) scaled x20 (outliers)."""
     x = torch.randn((m, k), device=dev, generator=g)
-    idx = torch.randperm(k, device=dev, generator=g)[: k // 100]
-    x[:, idx] *= 20.0
+    if outliers:
+        idx = torch.randperm(k, device=dev, generator=g)[: k // 100]
+        x[:, idx] *= 20.0
     return x.to(torch.bfloat16)
 
 
-def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool = False):
+def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool = False, specs=LINEARS,
+                   outliers: bool = True):
     """FP8Linear modules with their activations (and adaLN shift / scale [1, C] where the
     input is adaLN-modulated), and the Q/K/V (+ key mask) of each attention."""
     from minimaxh3_amd.kernels.fp8_linear import FP8Linear
@@ -115,7 +131,7 @@ def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool =
     g = torch.Generator(device=dev).manual_seed(0)
     linears = []
     if tokens:
-        for name, k, n, act in LINEARS:
+        for name, k, n, act in specs:
             lin = torch.nn.Linear(k, n, bias=True, device=dev, dtype=torch.bfloat16)
             with torch.no_grad():
                 lin.weight.copy_(torch.randn((n, k), device=dev, generator=g) * 0.02)
@@ -130,7 +146,7 @@ def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool =
             if adaln and name in ADALN_LINEARS:
                 mod_params = tuple((torch.randn((1, k), device=dev, generator=g) * 0.1).to(torch.bfloat16)
                                    for _ in range(2))
-            linears.append((name, mod, activations(torch, g, tokens, k, dev), mod_params))
+            linears.append((name, mod, activations(torch, g, tokens, k, dev, outliers), mod_params))
     attn_inputs = []
     for name, b, sq, sk, tail in attns:
         q = torch.randn((b, sq, HEADS, HEAD_DIM), device=dev, generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
@@ -172,12 +188,43 @@ class Timers:
         return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
 
 
-def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True, tau: float = -1.0):
+def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True, tau: float = -1.0,
+             chain: str | None = None):
     """One pass of the hot path; the same kernel calls FP8Linear.forward / fp8_attention make
-    (tau: the attention's repair threshold, < 0 for none)."""
+    (tau: the attention's repair threshold, < 0 for none).
+
+    chain: None runs every linear on its own activations and the attention on its own Q/K/V;
+    "stats" / "pass" make the (single) attention's q, k, v the [B, H, S, D] views of the QKV
+    projection's output and run it right after that projection, as a DiT block does, with
+    the K/V statistics from the projection's epilogue ("stats": gemm_rowwise_kv_stats +
+    attn_quant_kv_gemm_stats, K and V read once) or from their own pass ("pass":
+    attn_quant_kv)."""
     tick = timers.start if timers else (lambda n: None)
     tock = timers.stop if timers else (lambda t: None)
     outs = []
+
+    def attention(name, q, k, v, mask, part=None):
+        sfx = "" if name == "attn" else f"[{name}]"
+        c = ops.softmax_c(None, HEAD_DIM)
+        t = tick("attn_quant_kv" + sfx)
+        if part is None:
+            k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
+        else:
+            k8, sk, v8t, sv, _ = ops.attn_quant_kv_gemm_stats(k, v, part, None)
+        tock(t)
+        if fuse_q:
+            # the Q quantizer runs inside the attention launch
+            t = tick("attn_fwd" + sfx)
+            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, tau, k.shape[2]))
+            tock(t)
+        else:
+            t = tick("attn_quant_q" + sfx)
+            q8, sq = ops.attn_quant_q(q, c)
+            tock(t)
+            t = tick("attn_fwd" + sfx)
+            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, tau, q, k.shape[2]))
+            tock(t)
+
     for name, mod, x, mod_params in linears:
         if mod_params is None:
             t = tick(f"quant_rows[{name}]")
@@ -196,26 +243,22 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bo
             lt, lb, ls = mod._lora_operands(x)
             tock(t)
         t = tick(f"gemm[{name}]")
-        outs.append(ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), lt, lb, ls))
-        tock(t)
-    for name, q, k, v, mask in attn_inputs:
-        sfx = "" if name == "attn" else f"[{name}]"
-        c = ops.softmax_c(None, HEAD_DIM)
-        t = tick("attn_quant_kv" + sfx)
-        k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
-        tock(t)
-        if fuse_q:
-            # the Q quantizer runs inside the attention launch
-            t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, tau, k.shape[2]))
-            tock(t)
+        if chain == "stats" and name == "qkv":
+            out, part = ops.gemm_rowwise_kv_stats(x8, mod.w8, sa, mod.w_scale, mod.bias, x.shape[0], HIDDEN,
+                                                  2 * HIDDEN, HIDDEN)
         else:
-            t = tick("attn_quant_q" + sfx)
-            q8, sq = ops.attn_quant_q(q, c)
-            tock(t)
-            t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, tau, q, k.shape[2]))
-            tock(t)
+            out, part = ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), lt, lb, ls), None
+        tock(t)
+        outs.append(out)
+        if chain and name == "qkv":
+            (aname, q, k, v, mask), = attn_inputs
+            B, S = q.shape[0], q.shape[2]
+            qkv = out.view(B, S, 3, HEADS, HEAD_DIM)
+            q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+            attention(aname, q, k, v, mask, part)
+    if not chain:
+        for name, q, k, v, mask in attn_inputs:
+            attention(name, q, k, v, mask)
     return outs
 
 
@@ -255,10 +298,12 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(step_lin: float, step_att: float, runs: int = 5) -> dict:
+def cpu_baseline(step_lin: float, step_att: float, specs=LINEARS, full_tokens: int = 0, runs: int = 5) -> dict:
     """Reference CPU fallbacks on a bounded sample, scaled to the step's FLOP mix
-    (step_lin GEMM FLOPs, step_att attention FLOPs): the median of `runs` timed runs of each
-    part after one warmup run."""
+    (step_lin GEMM FLOPs of the linears `specs`, step_att attention FLOPs): the median of
+    `runs` timed runs of each part after one warmup run.  With `full_tokens` the linear
+    sample is the whole step's linears at that many tokens; otherwise 2048 of the DiT's
+    20280 tokens."""
     import statistics
 
     import torch
@@ -268,15 +313,15 @@ def cpu_baseline(step_lin: float, step_att: float, runs: int = 5) -> dict:
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    ms = 2048
+    ms = full_tokens or 2048
     lin = []
-    for _, k, n, _ in LINEARS:
+    for _, k, n, _ in specs:
         x = torch.randn((ms, k), generator=g).to(torch.bfloat16)
         w = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16)
         x8, sa = quantize_rows_torch(x)
         w8, sw = quantize_rows_torch(w)
         lin.append((x8, sa, w8, sw.view(1, -1), (torch.randn((n,), generator=g) * 0.01).to(torch.bfloat16)))
-    lin_flops = sum(gemm_flops(ms, n, k) for _, k, n, _ in LINEARS)
+    lin_flops = sum(gemm_flops(ms, n, k) for _, k, n, _ in specs)
     hs = 2
     q, k, v = (torch.randn((1, hs, TOKENS, HEAD_DIM), generator=g) for _ in range(3))
     at_flops = attn_flops(1, hs, TOKENS, TOKENS, HEAD_DIM)
@@ -290,21 +335,27 @@ def cpu_baseline(step_lin: float, step_att: float, runs: int = 5) -> dict:
             ts.append(time.perf_counter() - t0)
         return statistics.median(ts)
 
-    # the linear sample is skipped for a workload without linears
+    # a part the step does not have is not sampled
     t_lin = median_time(lambda: [dequant_linear(*a) for a in lin]) if step_lin else float("inf")
-    t_att = median_time(lambda: sdpa_fallback(q, k, v))
+    t_att = median_time(lambda: sdpa_fallback(q, k, v)) if step_att else float("inf")
     lin_rate, att_rate = lin_flops / t_lin, at_flops / t_att
-    step_s = (step_lin / lin_rate if step_lin else 0.0) + step_att / att_rate
+    step_s = (step_lin / lin_rate if step_lin else 0.0) + (step_att / att_rate if step_att else 0.0)
+    if full_tokens and not step_att:
+        sample = (f"median of {runs} runs after a warmup: torch CPU fp32 dequant-matmul of the whole step "
+                  f"({len(specs)} linear(s) at {ms} tokens, {lin_flops / 1e9:.2f} GFLOP, {t_lin * 1e3:.1f} ms); "
+                  f"host {cpu_model()}, {cores} threads")
+    else:
+        sample = (f"median of {runs} runs after a warmup: torch CPU fp32 dequant-matmul of the {len(specs)} DiT "
+                  f"linears on {ms} of {TOKENS} tokens ({lin_rate / 1e12:.3f} TFLOP/s) and fp32 SDPA on {hs} of "
+                  f"{HEADS} heads at S={TOKENS} ({att_rate / 1e12:.3f} TFLOP/s); value = the step's FLOPs over the "
+                  f"step time these rates imply ({step_s:.1f} s, heads scaled x{HEADS // hs}); host {cpu_model()}, "
+                  f"{cores} threads")
     return {
         "value": round((step_lin + step_att) / step_s / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"median of {runs} runs after a warmup: torch CPU fp32 dequant-matmul of the 4 DiT linears on "
-                   f"{ms} of {TOKENS} tokens ({lin_rate / 1e12:.3f} TFLOP/s) and fp32 SDPA on {hs} of {HEADS} heads "
-                   f"at S={TOKENS} ({att_rate / 1e12:.3f} TFLOP/s); value = the step's FLOPs over the step time "
-                   f"these rates imply ({step_s:.1f} s, heads scaled x{HEADS // hs}); host {cpu_model()}, "
-                   f"{cores} threads"),
+        "sample": sample,
     }
 
 
@@ -327,11 +378,12 @@ def _csv_rows(directory: str, suffix: str):
         return list(csv.DictReader(f))
 
 
-def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
+def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",), gemm_names=("qkv", "attn_out", "mlp_down")):
     """dispatch id -> part name for the DiT-block kernels of this script's steps, in dispatch
-    order: the three no-activation GEMMs of a step are QKV, attention-out, MLP-down (MLP-up
-    is the GELU instance); activation quantizers are told from the weight quantizers at
-    set-up by their grid (one 256-thread block per 4 rows of the workload's tokens)."""
+    order: the no-activation GEMMs of a step are `gemm_names` in turn (the DiT block's QKV,
+    attention-out, MLP-down; MLP-up is the GELU instance); activation quantizers are told from
+    the weight quantizers at set-up by their grid (one 256-thread block per 4 rows of the
+    workload's tokens)."""
     act_grid = str(math.ceil(tokens / 4) * 256)
     out, k = {}, 0
     na = len(attn_names)
@@ -345,7 +397,7 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
             if act and act.group(1) == "1":  # the GELU-tanh epilogue
                 out[d] = "gemm[mlp_up]"
             else:
-                out[d] = ("gemm[qkv]", "gemm[attn_out]", "gemm[mlp_down]")[k % 3]
+                out[d] = f"gemm[{gemm_names[k % len(gemm_names)]}]"
                 k += 1
         elif "quant_rows_reg_kernel" in name and grid == act_grid:
             out[d] = "quant_rows<0, 24>[mlp_down]" if "<0, 24" in name else "quant_rows<0, 6>"
@@ -359,7 +411,7 @@ def _labels(dispatches, tokens: int = TOKENS, attn_names=("attn",)):
             ka += 1
         elif "attn_kv_colreduce_kernel" in name:
             out[d] = "attn_quant_kv: colreduce" + sfx(kq)
-        elif "attn_kv_fold_kernel" in name:
+        elif "attn_kv_fold_kernel" in name or "gemm_kv_stats_fold_kernel" in name:
             out[d] = "attn_quant_kv: fold" + sfx(kq)
         elif "attn_quant_kv_kernel" in name:
             out[d] = "attn_quant_kv: quantize" + sfx(kq)
@@ -383,7 +435,8 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
     rows = _csv_rows(directory, "kernel_trace.csv")
     disp = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X"))) for r in rows)
     names = tuple(a[0] for a in attns)
-    lab = _labels(disp, tokens or TOKENS, names)
+    gemm_names = tuple(n for n, _, _, act in linears_of(workload) if act == 0)
+    lab = _labels(disp, tokens or TOKENS, names, gemm_names)
     dur = {}
     for r in rows:
         d = int(r["Dispatch_Id"])
@@ -397,6 +450,7 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
     if len(names) > 1:
         order += [f"{base}[{n}]" for n in names for base in ("attn_quant_kv: colreduce", "attn_quant_kv: fold",
                                                               "attn_quant_kv: quantize", "attn_fwd")]
+    order += sorted(p for p in dur if p not in order)
     lines = ["| part | launches | median us | mean us | min us | max us |", "|---|---|---|---|---|---|"]
     for p in order:
         if p in dur:
@@ -414,6 +468,14 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
                      f"TFLOP per launch / {med:.1f} us (median launch) = {f / (med * 1e-6) / 1e12:.1f} TFLOP/s = "
                      f"{f / (med * 1e-6) / 1e12 / PEAK_FP8_TFLOPS:.4f} of the {PEAK_FP8_TFLOPS:.0f} TFLOP/s dense "
                      f"FP8 peak.")
+    for name, k, n, _ in (linears_of(workload) if tokens else ()):
+        key = f"gemm[{name}]"
+        if key in dur:
+            med = median(dur[key])
+            f = gemm_flops(tokens, n, k)
+            lines.append(f"`{key}` recomputed from this trace: 2 x {tokens} x {n} x {k} = {f / 1e12:.4f} TFLOP / "
+                         f"{med:.1f} us (median launch) = {f / (med * 1e-6) / 1e12:.1f} TFLOP/s = "
+                         f"{f / (med * 1e-6) / 1e12 / PEAK_FP8_TFLOPS:.4f} of peak.")
     return "\n".join(lines)
 
 
@@ -494,6 +556,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--separate-q-quant", action="store_true",
                     help="quantize Q in its own launch instead of inside the attention launch")
+    ap.add_argument("--chain", choices=("stats", "pass"),
+                    help="dit480 only: the attention's q, k, v are the QKV projection's output (views of "
+                         "[1, S, 3, H, D]), its K/V statistics from the projection's epilogue (stats) or from "
+                         "their own pass over K and V (pass)")
     ap.add_argument("--repair-tau", type=float, default=-1.0,
                     help="exact repair of P codes >= tau in every attention (the reference's quality "
                          "profile uses 0.5); < 0 disables it (default)")
@@ -525,33 +591,63 @@ def main() -> int:
     _native.load()
     _native.require_gfx950(dev)
     desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]
+    specs = linears_of(args.workload)
     fuse_q = not args.separate_q_quant
     tau = float(args.repair_tau)
+    chain = args.chain
+    if chain and args.workload != "dit480":
+        print("--chain applies to --workload dit480 only", file=sys.stderr)
+        return 2
+    if chain:
+        desc += (f"; chained: the attention reads the QKV projection's output, K/V statistics "
+                 f"{'from its epilogue' if chain == 'stats' else 'from their own pass'}")
     log("[bench] HBM streaming reference")
     stream_ref = hbm_stream_reference(torch, dev)
     log(f"[bench] building workload {args.workload}")
-    linears, attn_inputs = build_workload(torch, dev, tokens, lora_rank, attns, adaln)
+    linears, attn_inputs = build_workload(torch, dev, tokens, lora_rank, attns, adaln, specs,
+                                          args.workload not in NO_OUTLIERS)
     torch.cuda.synchronize()
 
+    def step(timers=None):
+        return run_step(torch, ops, linears, attn_inputs, timers, fuse_q, tau, chain)
+
+    graphed = args.workload in GRAPHED
     with torch.inference_mode():
         for i in range(args.warmup):
-            run_step(torch, ops, linears, attn_inputs, None, fuse_q, tau)
+            step()
         torch.cuda.synchronize()
-        log(f"[bench] warmup done ({args.warmup} steps)")
+        graph = None
+        if graphed:
+            # one step captured on a side stream, replayed as one launch per step
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            for _ in range(args.warmup):
+                graph.replay()
+            torch.cuda.synchronize()
+        log(f"[bench] warmup done ({args.warmup} steps{', then a captured step replayed as often' if graphed else ''})")
         # The timed steps bracket only the attention launches (the roofline kernel) with HIP
         # events: an event pair around every launch adds ~0.1 ms to a 5 ms step.
         roof_timers = Timers(torch, prefix="attn_fwd")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, roof_timers, fuse_q, tau)
+            if graph is not None:
+                graph.replay()
+            else:
+                step(roof_timers)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
         # per-launch breakdown: the same steps again, every launch bracketed (not timed)
         timers = Timers(torch)
         for _ in range(args.steps):
-            run_step(torch, ops, linears, attn_inputs, timers, fuse_q, tau)
+            step(timers)
         torch.cuda.synchronize()
     ms_step = elapsed * 1e3 / args.steps
     kern = timers.mean_ms()
@@ -565,11 +661,14 @@ def main() -> int:
 
     parts = {}
     gemm_f = gemm_ms = 0.0
-    for name, k, n, _ in (LINEARS if tokens else ()):
+    biggest_gemm = None
+    for name, k, n, _ in (specs if tokens else ()):
         f = gemm_flops(tokens, n, k)
         gemm_f += f
         gemm_ms += kern[f"gemm[{name}]"]
         parts[f"gemm[{name}]"] = flop_part(f, kern[f"gemm[{name}]"])
+        if biggest_gemm is None or f > biggest_gemm[1]:
+            biggest_gemm = (f"gemm[{name}]", f, kern[f"gemm[{name}]"])
         if lora_rank:
             # the rank-r up-projection runs in the GEMM epilogue (not in its FLOP count)
             parts[f"gemm[{name}]"]["lora_tflop"] = round(2.0 * tokens * lora_rank * n / 1e12, 4)
@@ -608,8 +707,14 @@ def main() -> int:
     att_ms = attn_ms + sum(v for k, v in kern.items() if k.startswith("attn_quant"))
     step_flops = gemm_f + attn_f
     value = step_flops / (ms_step * 1e-3) / 1e12
-    _, af, t_attn = biggest
-    achieved = af / (t_attn * 1e-3) / 1e12
+    if biggest is not None:
+        roof_name, roof_f, roof_t = biggest
+        roof_kernel = f"{roof_name}: attn_fwd_kernel<128,...>"
+    else:
+        # no attention in the step: the largest GEMM (its per-launch event time)
+        roof_name, roof_f, roof_t = biggest_gemm
+        roof_kernel = f"{roof_name}: gemm_fp8_rowwise_kernel"
+    achieved = roof_f / (roof_t * 1e-3) / 1e12
 
     line = {
         "metric": METRIC,
@@ -629,31 +734,34 @@ def main() -> int:
             "tokens": tokens or None, "hidden": HIDDEN, "mlp": MLP, "heads": HEADS, "head_dim": HEAD_DIM,
             "lora_rank": lora_rank or None,
             "repair_tau": tau if tau >= 0 else None,
+            "chain": chain,
+            "graph_replay": graphed,
             "step_tflop": round(step_flops / 1e12, 4),
         },
         "frac_of_fp8_peak": round(value / PEAK_FP8_TFLOPS, 4),
         "gemm_tflops": round(gemm_f / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
-        "attn_tflops": round(attn_f / (attn_ms * 1e-3) / 1e12, 1),
+        "attn_tflops": round(attn_f / (attn_ms * 1e-3) / 1e12, 1) if attn_ms else None,
         "end_to_end": {
             "linear": {"ms": round(lin_ms, 4), "TFLOP/s": round(gemm_f / (lin_ms * 1e-3) / 1e12, 1)} if lin_ms else None,
-            "attention": {"ms": round(att_ms, 4), "TFLOP/s": round(attn_f / (att_ms * 1e-3) / 1e12, 1)},
+            "attention": ({"ms": round(att_ms, 4), "TFLOP/s": round(attn_f / (att_ms * 1e-3) / 1e12, 1)}
+                          if att_ms else None),
         },
         "roofline": {
-            "kernel": f"{biggest[0]}: attn_fwd_kernel<128,...>",
+            "kernel": roof_kernel,
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": PEAK_FP8_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             # counter-measured for the 480p attention only
-            "traffic": round(ATTN_TRAFFIC_BYTES) if args.workload == "dit480" else None,
+            "traffic": round(ATTN_TRAFFIC_BYTES) if args.workload == "dit480" and not chain else None,
         },
         "kernels": parts,
         "hbm_stream_reference": stream_ref,
     }
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline")
-        line["cpu_baseline"] = cpu_baseline(gemm_f, attn_f)
+        line["cpu_baseline"] = cpu_baseline(gemm_f, attn_f, specs, tokens if args.workload in LINEAR_SETS else 0)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -92,6 +92,32 @@ int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const float* sa, con
                       void* out, int64_t M, int64_t N, int64_t K, int64_t ld_out,
                       hipStream_t stream);
 
+/* Bytes of the K/V column statistics that mxf8_gemm_rowwise_kv_stats writes for M rows and
+ * C columns per part: 2 statistics x ceil(M/128) blocks x C fp32. */
+int64_t mxf8_gemm_kv_stats_bytes(int64_t M, int64_t C);
+
+/*
+ * mxf8_gemm_rowwise (no LoRA, no activation) of a fused QKV projection that also emits the
+ * column statistics of its key and value parts, so that the attention's K/V quantizers
+ * read K and V once.  Replaces k.float().mean(dim=2) (kernels/fp8_attention.py:338) and the
+ * first pass of _quantize_v_kernel (122-155, the per-channel |max| over the sequence),
+ * taken over the bf16 outputs as they are stored.
+ *   out [M, N] bf16 is mxf8_gemm_rowwise's output bit for bit; rows of batch item b are
+ *   [b S, (b + 1) S) (M % S == 0, S >= 128).
+ *   Key columns [k_col0, k_col0 + C) (k_col0 < 0: none): per-channel sums; value columns
+ *   [v_col0, v_col0 + C) (v_col0 < 0: none): per-channel |max| (NaN skipped).
+ *   part (written, mxf8_gemm_kv_stats_bytes(M, C) bytes): [2][ceil(M/128)][C] fp32, the
+ *   statistic of each 128-row block p that lies inside one batch item; the blocks holding an
+ *   item boundary or row M are not written (mxf8_attn_quant_kv_gemm_stats reads their rows).
+ *   Fixed order.
+ * Requires N % 256 == 0, ld_out % 8 == 0 (ld_out >= N), 16-byte aligned out, a8, w8 and
+ * part, C % 256 == 0, column ranges starting at multiples of 256 inside [0, N), K % 16 == 0.
+ */
+int mxf8_gemm_rowwise_kv_stats(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
+                               const void* bias, void* out, int64_t M, int64_t N, int64_t K, int64_t ld_out,
+                               int64_t S, int64_t k_col0, int64_t v_col0, int64_t C, float* part,
+                               hipStream_t stream);
+
 /*
  * LoRA down-projection t = bf16(x A^T) used by the LoRA epilogue (the first matmul of
  * apply_lora_adapters, kernels/fp8_linear.py:53).
@@ -167,6 +193,25 @@ int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], const void* v,
                        int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                        uint8_t* k8, float* sk, uint8_t* v8t, float* sv, float* mean, void* workspace,
                        hipStream_t stream);
+
+/*
+ * K and V quantizers fed by the QKV projection's column statistics: the key mean
+ * (kernels/fp8_attention.py:338), _quantize_k_kernel (80-119) and _quantize_v_kernel
+ * (122-170) of one attention call whose k and v are views of the output of
+ * mxf8_gemm_rowwise_kv_stats (rows b S + s, key / value columns h D + d of its parts).  One
+ * fold launch turns `part` (and the rows of the blocks it leaves out, at most two per batch
+ * item) into the key mean and the V scales, one pass quantizes K and V: K and V are read
+ * once.
+ *   part: the statistics written by mxf8_gemm_rowwise_kv_stats (M = B S, C = H D).
+ *   key_stats != 0: the key mean comes from part's key sums (mean written); key_stats == 0:
+ *   `mean` [B, H, D] fp32 is an input (e.g. mxf8_attn_kmean of keys transformed after the
+ *   projection), and only the V statistics are taken from part.
+ *   Other arguments and outputs as mxf8_attn_quant_kv; requires S >= 128, (H D) % 256 == 0.
+ */
+int mxf8_attn_quant_kv_gemm_stats(const void* k, const int64_t k_strides[4], const void* v,
+                                  const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S,
+                                  int64_t D, const float* part, int key_stats, uint8_t* k8, float* sk,
+                                  uint8_t* v8t, float* sv, float* mean, hipStream_t stream);
 
 /*
  * mxf8_attn_quant_kv without a workspace argument and without any device allocation.  No

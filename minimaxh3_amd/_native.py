@@ -33,6 +33,9 @@ _SIGNATURES = {
     "mxf8_adaln_quant_rows": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _f32, _i32, _vp, _vp, _vp, _vp]),
     "mxf8_gemm_rowwise": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _f32, _vp, _i64, _i64, _i64, _i64,
                                  _vp]),
+    "mxf8_gemm_kv_stats_bytes": (_i64, [_i64, _i64]),
+    "mxf8_gemm_rowwise_kv_stats": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                          _i64, _vp, _vp]),
     "mxf8_lora_down": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     "mxf8_attn_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "mxf8_attn_quant_q": (_i32, [_vp, _i32, _I64x4, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
@@ -42,7 +45,9 @@ _SIGNATURES = {
     "mxf8_attn_kv_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "mxf8_attn_quant_kv": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _vp]),
-    "mxf8_attn_quant_kv_noalloc": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+    "mxf8_attn_quant_kv_gemm_stats": (_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _i32,
+                                             _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mxf8_attn_quant_kv_noalloc":(_i32, [_vp, _I64x4, _vp, _I64x4, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                           _vp, _vp]),
     "mxf8_attn_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i32, _I64x4, _i64, _i64, _i64, _i64,
                              _i64, _i32, _vp]),

@@ -24,6 +24,6 @@ int check_launch(const char* what) {
 
 }  // namespace mxf8
 
-extern "C" int mxf8_abi_version(void) { return 200; }
+extern "C" int mxf8_abi_version(void) { return 201; }
 
 extern "C" const char* mxf8_last_error(void) { return mxf8::g_last_error; }

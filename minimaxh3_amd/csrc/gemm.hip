@@ -24,6 +24,8 @@
 // the start of the tile), so neither the pipeline fill nor a workgroup launch separates
 // two tiles.  A whole output tile (no LoRA) is staged through the freed stage buffer and
 // written as 16-byte stores of whole row segments.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mxf8 {
@@ -192,6 +194,25 @@ __device__ __forceinline__ v8bf lds_chunk_bf16(const uint8_t* tile, int row, int
 // memory in the epilogue (r > 128).
 enum { LORA_NONE = 0, LORA_LDS = 1, LORA_GLOBAL = 2 };
 
+// Column statistics of a fused QKV projection's K and V parts (the kernel's KVS mode): the
+// attention's K quantizer needs the key mean over each batch item's whole sequence and the
+// V quantizer the per-channel |max| over it (kernels/fp8_attention.py:338 and 140-155), so
+// the epilogue emits both over the bf16 outputs it stores, per 128-row block of tokens:
+//   part[0][p][c] = sum of out[m, kc0 + c],   part[1][p][c] = max |out[m, vc0 + c]|
+// over the rows m of block p, [128 p, 128 p + 128), for every block that lies inside one batch
+// item (S rows each) and below M.  The other blocks -- at most two per item, where an item
+// boundary or M falls inside them -- are left to the consumer, which reads their rows.
+// Fixed order throughout, so the statistics do not depend on scheduling.
+struct KvStats {
+  float* part;  // [2][nb][C] fp32
+  int kc0;      // first key column, or -1 (no key sums)
+  int vc0;      // first value column, or -1 (no value maxima)
+  int C;        // columns of each part (heads x head dim), a multiple of 256
+  int S;        // rows per batch item
+  int nb;       // 128-row blocks, ceil(M / 128)
+};
+constexpr int KVS_BLOCK = 128;
+
 // LoRA branch of one 32x32 output block from a LoRA chunk staged like a K stage (B rows
 // [BN x 128 bytes], then t rows [BM x 128 bytes]; 64 rank columns in bf16):
 // lacc^T[n][m] += sum_j B[n][j] t[m][j].  K step j reads logical chunk 2j + g of both.
@@ -218,12 +239,17 @@ __device__ __forceinline__ v4f quad4(const v16f& c, int q) {
 // like K stages: the first chunk during the last K stage, into the buffer the next tile's
 // first stage would otherwise take; that stage then goes into the buffer the last K
 // stage frees, so it still overlaps the epilogue.
-template <class C, int ACT, int LM, bool KTAIL>
+// KVS (no LoRA, no activation): the K/V column statistics above, taken from the staged
+// output rows of whole-channel tiles (the host guarantees N % 256 == 0, 16-byte rows).
+template <class C, int ACT, int LM, bool KTAIL, bool KVS = false>
 __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
     const uint8_t* __restrict__ a8, const uint8_t* __restrict__ w8, const float* __restrict__ sa,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ lora_t,
     const uint16_t* __restrict__ lora_b, int lora_r, float lora_scale, uint16_t* __restrict__ out, int M, int N,
-    int K, int64_t ld_out, int tiles_m, int tiles_n, int group_m) {
+    int K, int64_t ld_out, int tiles_m, int tiles_n, int group_m, KvStats kvs) {
+  static_assert(!KVS || (LM == LORA_NONE && ACT == MXF8_ACT_NONE), "K/V statistics: plain epilogue only");
+  static_assert(!KVS || C::WM * (C::BM / C::WM) == C::BM && C::BM / C::WM * 2 == KVS_BLOCK,
+                "K/V statistics: two waves per 128-row block");
   constexpr int TM = C::TM, TN = C::TN;
   constexpr int EP_BYTES = (2 * C::BN + C::BM) * 4;  // channel scales, bias (fp32), token scales
   // with LoRA chunks in LDS: each wave's 2 KB output staging region (one 32 x 32 block)
@@ -469,8 +495,10 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
       return make_uint2(bf16x2(v[0], v[1]), bf16x2(v[2], v[3]));
     };
 
-    const bool staged =
-        ((ld_out & 7) == 0) && ((((uintptr_t)out) & 15) == 0) && (m0 + C::BM <= M) && (n0 + C::BN <= N);
+    // (KVS: every tile is staged -- the host checks the row alignment and that N is a multiple
+    // of 256 -- token-tail tiles included, whose rows past M are not stored)
+    const bool staged = KVS || (((ld_out & 7) == 0) && ((((uintptr_t)out) & 15) == 0) && (m0 + C::BM <= M) &&
+                                (n0 + C::BN <= N));
     if (staged && LM != LORA_LDS) {
       // Whole tile in range: each 32-token round of this wave goes through a private 8 KB
       // LDS region in the buffer of the last K stage (free after the barrier above; the
@@ -482,27 +510,147 @@ __global__ __launch_bounds__(C::THREADS) void gemm_fp8_rowwise_kernel(
       static_assert(32 * RB <= C::STAGE / C::NW, "per-wave staging region");
       uint8_t* const wreg = smem + ((gs + 1) & 1) * C::STAGE + wave * (C::STAGE / C::NW);
       const int r = lane & 31;
+      // KVS: kv = 1 on key columns (sums), 2 on value columns (|max|), 0 elsewhere (uniform
+      // over the workgroup).  A lane reads channels n0 + wrow0 + 8 (lane % NCH) + [0, 8) of
+      // its rows and keeps their running statistic (ks) when the wave's 128-row block lies
+      // inside one batch item and below M (kvx = kv there, else 0: no statistic).
+      int kv = 0, kvx = 0;
+      float ks[8];
+      if constexpr (KVS) {
+        kv = kvs.kc0 >= 0 && n0 >= kvs.kc0 && n0 < kvs.kc0 + kvs.C   ? 1
+             : kvs.vc0 >= 0 && n0 >= kvs.vc0 && n0 < kvs.vc0 + kvs.C ? 2
+                                                                       : 0;
+        const int b0 = (m0 + xrow0) & ~(KVS_BLOCK - 1);
+        kvx = b0 + KVS_BLOCK <= min((b0 / kvs.S + 1) * kvs.S, M) ? kv : 0;
 #pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        const float sam = ep_sa[xrow0 + 32 * b + r];
+        for (int e = 0; e < 8; ++e) ks[e] = 0.0f;
+      }
+      // One 32-token round: outputs -> LDS, then 16-byte rows out (rows past M are not stored
+      // in KVS mode), folding each chunk into the statistic ST (0 none, 1 sum, 2 |max|).
+      // The lane index behind the staging addresses is opaque to the compiler here, so the
+      // ~24 per-lane addresses derived from it are recomputed in each tile's epilogue rather
+      // than held in registers across the persistent loop (with the statistics live they would
+      // not fit and would go to scratch, whose reloads wait for every store in flight).
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int rk = ln & 31, gk = ln >> 5;
+      auto round = [&](int b, auto st_tag) {
+        constexpr int ST = decltype(st_tag)::value;
+        const float sam = ep_sa[xrow0 + 32 * b + rk];
 #pragma unroll
         for (int a = 0; a < TN; ++a) {
           const v16f lacc = lora_block(a, b);
           const int nl_ = wrow0 + 32 * a;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<uint2*>(wreg + r * RB + (((4 * a + q) ^ (r & (NCH - 1))) << 4) + 8 * g) =
-                out_quad(quad4(acc[a][b], q), q, lacc, sam, *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g),
-                         *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g));
+            *reinterpret_cast<uint2*>(wreg + rk * RB + (((4 * a + q) ^ (rk & (NCH - 1))) << 4) + 8 * gk) =
+                out_quad(quad4(acc[a][b], q), q, lacc, sam,
+                         *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * gk),
+                         *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * gk));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < 32 / RPI; ++i) {
-          const int row = i * RPI + lane / NCH, ch = lane % NCH;
+          const int row = i * RPI + ln / NCH, ch = ln % NCH;
           const uint4 val = *reinterpret_cast<const uint4*>(wreg + row * RB + ((ch ^ (row & (NCH - 1))) << 4));
-          store_out16(out + (int64_t)(m0 + xrow0 + 32 * b + row) * ld_out + n0 + wrow0 + ch * 8, val);
+          const int grow = m0 + xrow0 + 32 * b + row;
+          if (!KVS || grow < M) store_out16(out + (int64_t)grow * ld_out + n0 + wrow0 + ch * 8, val);
+          if constexpr (ST != 0) {
+            const uint32_t w4[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo = __uint_as_float(w4[e] << 16), hi = __uint_as_float(w4[e] & 0xffff0000u);
+              if constexpr (ST == 1) {
+                ks[2 * e] += lo;
+                ks[2 * e + 1] += hi;
+              } else {
+                ks[2 * e] = fmaxf(ks[2 * e], fabsf(lo));
+                ks[2 * e + 1] = fmaxf(ks[2 * e + 1], fabsf(hi));
+              }
+            }
+          }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      };
+      if constexpr (!KVS) {
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const float sam = ep_sa[xrow0 + 32 * b + r];
+#pragma unroll
+          for (int a = 0; a < TN; ++a) {
+            const v16f lacc = lora_block(a, b);
+            const int nl_ = wrow0 + 32 * a;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<uint2*>(wreg + r * RB + (((4 * a + q) ^ (r & (NCH - 1))) << 4) + 8 * g) =
+                  out_quad(quad4(acc[a][b], q), q, lacc, sam,
+                           *reinterpret_cast<const v4f*>(ep_sw + nl_ + 8 * q + 4 * g),
+                           *reinterpret_cast<const v4f*>(ep_b + nl_ + 8 * q + 4 * g));
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int i = 0; i < 32 / RPI; ++i) {
+            const int row = i * RPI + lane / NCH, ch = lane % NCH;
+            const uint4 val = *reinterpret_cast<const uint4*>(wreg + row * RB + ((ch ^ (row & (NCH - 1))) << 4));
+            store_out16(out + (int64_t)(m0 + xrow0 + 32 * b + row) * ld_out + n0 + wrow0 + ch * 8, val);
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      } else {
+        typedef std::integral_constant<int, 0> St0;
+        typedef std::integral_constant<int, 1> St1;
+        typedef std::integral_constant<int, 2> St2;
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          if (kvx == 0)
+            round(b, St0{});
+          else if (kvx == 1)
+            round(b, St1{});
+          else
+            round(b, St2{});
+        }
+      }
+      if constexpr (KVS) {
+        if (kv != 0) {
+          // Lanes with one lane % NCH read the same channels: combine them (a fixed
+          // butterfly), then the two waves of each 128-row block through LDS (each wave's
+          // own staging region, free now), in wave order.
+          if (kvx != 0) {
+#pragma unroll
+            for (int off = NCH; off < 64; off <<= 1) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float o = __shfl_xor(ks[e], off, 64);
+                ks[e] = kvx == 1 ? ks[e] + o : fmaxf(ks[e], o);
+              }
+            }
+            if (lane < NCH) {
+              float* dst = reinterpret_cast<float*>(wreg) + 8 * lane;
+              *reinterpret_cast<v4f*>(dst) = v4f{ks[0], ks[1], ks[2], ks[3]};
+              *reinterpret_cast<v4f*>(dst + 4) = v4f{ks[4], ks[5], ks[6], ks[7]};
+            }
+          }
+          block_barrier();
+          // thread t: tile channel t of wave column t / (BN / WN); waves 2h, 2h + 1 of that
+          // column hold 128-row block h of the tile
+          constexpr int CPW = C::BN / C::WN;  // channels per wave
+          const int t = threadIdx.x;
+          if (t < C::BN) {
+            const int wn_t = t / CPW, c_in = t % CPW;
+            const int col0 = kv == 1 ? kvs.kc0 : kvs.vc0;
+            float* const pst = kvs.part + (int64_t)(kv - 1) * kvs.nb * kvs.C + (n0 - col0 + t);
+#pragma unroll
+            for (int h = 0; h < C::BM / KVS_BLOCK; ++h) {
+              const int p = (m0 >> 7) + h, b0 = p * KVS_BLOCK;
+              if (b0 + KVS_BLOCK <= min((b0 / kvs.S + 1) * kvs.S, M)) {
+                const float* ra = reinterpret_cast<const float*>(smem + ((gs + 1) & 1) * C::STAGE +
+                                                                 (wn_t * C::WM + 2 * h) * (C::STAGE / C::NW)) + c_in;
+                const float x0 = ra[0], x1 = ra[(C::STAGE / C::NW) / 4];
+                pst[(int64_t)p * kvs.C] = kv == 1 ? x0 + x1 : fmaxf(x0, x1);
+              }
+            }
+          }
+        }
       }
     } else if (staged) {
       // LoRA chunks and the next tile's first stage fill both stage buffers: each 32 x 32
@@ -718,10 +866,10 @@ __global__ __launch_bounds__(64 * W) void lora_down_kernel(const uint8_t* __rest
 }
 
 
-template <class C, int ACT, int LM, bool KTAIL>
+template <class C, int ACT, int LM, bool KTAIL, bool KVS = false>
 static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
                         const uint16_t* bias, const uint16_t* lt, const uint16_t* lb, int r, float ls, uint16_t* out,
-                        int M, int N, int K, int64_t ld_out, hipStream_t st) {
+                        int M, int N, int K, int64_t ld_out, hipStream_t st, const KvStats& kvs = KvStats{}) {
   const int tiles_m = (int)cdiv(M, C::BM), tiles_n = (int)cdiv(N, C::BN);
   const int ntiles = tiles_m * tiles_n;
   // Persistent grid: as many workgroups as stay resident (LDS decides: one per CU for the
@@ -735,8 +883,8 @@ static void launch_gemm(const uint8_t* a8, const uint8_t* w8, const float* sa, c
   // with 2 and 602 with 1), the K = 3072 ones in groups of 8 (out-projection and MLP-up 1-2%
   // ahead of 4 and 16; QKV within 1.5% from 4 to 16).
   const int group_m = K >= 8192 ? 4 : 8;
-  gemm_fp8_rowwise_kernel<C, ACT, LM, KTAIL><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
-      a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n, group_m);
+  gemm_fp8_rowwise_kernel<C, ACT, LM, KTAIL, KVS><<<dim3(grid), dim3(C::THREADS), 0, st>>>(
+      a8, w8, sa, sw, bias, lt, lb, r, ls, out, M, N, K, ld_out, tiles_m, tiles_n, group_m, kvs);
 }
 
 template <class C>
@@ -806,6 +954,62 @@ extern "C" int mxf8_gemm_rowwise(const uint8_t* a8, const uint8_t* w8, const flo
   return check_launch("gemm_rowwise");
 }
 
+extern "C" int64_t mxf8_gemm_kv_stats_bytes(int64_t M, int64_t C) {
+  if (M <= 0 || C <= 0) return 0;
+  return 2 * cdiv(M, KVS_BLOCK) * C * (int64_t)sizeof(float);
+}
+
+extern "C" int mxf8_gemm_rowwise_kv_stats(const uint8_t* a8, const uint8_t* w8, const float* sa, const float* sw,
+                                          const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                                          int64_t ld_out, int64_t S, int64_t k_col0, int64_t v_col0, int64_t C,
+                                          float* part, hipStream_t stream) {
+  const char* what = "gemm_rowwise_kv_stats";
+  if (M <= 0 || N <= 0 || K <= 0) return set_error(MXF8_EINVAL, "%s: empty or negative shape", what);
+  if (!a8 || !w8 || !sa || !sw || !out || !part) return set_error(MXF8_EINVAL, "%s: null pointer", what);
+  if (K % 16) return set_error(MXF8_EINVAL, "%s: K=%lld must be a multiple of 16", what, (long long)K);
+  if (M > (1 << 30) || N > 0x7fffffff / 2 || K > (1 << 22)) return set_error(MXF8_EINVAL, "%s: shape too large", what);
+  // whole 256-channel tiles and 16-byte output rows: every tile leaves through the staged stores
+  if (N % 256 || ld_out < N || ld_out % 8 || ((uintptr_t)out % 16))
+    return set_error(MXF8_EINVAL, "%s: N and ld_out must be multiples of 256 and 8 (ld_out >= N), out 16-byte "
+                     "aligned", what);
+  if (((uintptr_t)a8 % 16) || ((uintptr_t)w8 % 16) || ((uintptr_t)part % 16))
+    return set_error(MXF8_EINVAL, "%s: a8, w8 and part must be 16-byte aligned", what);
+  if (S < KVS_BLOCK || M % S)
+    return set_error(MXF8_EINVAL, "%s: S=%lld must be >= %d and divide M=%lld", what, (long long)S, KVS_BLOCK,
+                     (long long)M);
+  if (C <= 0 || C % 256) return set_error(MXF8_EINVAL, "%s: C=%lld must be a positive multiple of 256", what,
+                                          (long long)C);
+  if (k_col0 < 0 && v_col0 < 0) return set_error(MXF8_EINVAL, "%s: neither key nor value columns given", what);
+  for (const int64_t c0 : {k_col0, v_col0})
+    if (c0 >= 0 && (c0 % 256 || c0 + C > N))
+      return set_error(MXF8_EINVAL, "%s: a column range must start at a multiple of 256 and end by N", what);
+  if (k_col0 >= 0 && v_col0 >= 0 && k_col0 < v_col0 + C && v_col0 < k_col0 + C)
+    return set_error(MXF8_EINVAL, "%s: key and value column ranges overlap", what);
+  KvStats kvs;
+  kvs.part = part;
+  kvs.kc0 = k_col0 < 0 ? -1 : (int)k_col0;
+  kvs.vc0 = v_col0 < 0 ? -1 : (int)v_col0;
+  kvs.C = (int)C;
+  kvs.S = (int)S;
+  kvs.nb = (int)cdiv(M, KVS_BLOCK);
+  const int iM = (int)M, iN = (int)N, iK = (int)K;
+  const uint16_t* b16 = static_cast<const uint16_t*>(bias);
+  uint16_t* o16 = static_cast<uint16_t*>(out);
+  const bool ktail = (K % GEMM_BK) != 0;
+  // the tile choice of mxf8_gemm_rowwise, so the output is that entry point's bit for bit
+  const bool big = cdiv(M, 256) * cdiv(N, 256) >= 2 * 256;
+#define MXF8_KVS_LAUNCH(Cfg, T)                                                                                    \
+  launch_gemm<Cfg, MXF8_ACT_NONE, LORA_NONE, T, true>(a8, w8, sa, sw, b16, nullptr, nullptr, 0, 0.0f, o16, iM, iN, \
+                                                      iK, ld_out, stream, kvs)
+  if (big) {
+    if (ktail) MXF8_KVS_LAUNCH(GemmBig, true); else MXF8_KVS_LAUNCH(GemmBig, false);
+  } else {
+    if (ktail) MXF8_KVS_LAUNCH(GemmSmall, true); else MXF8_KVS_LAUNCH(GemmSmall, false);
+  }
+#undef MXF8_KVS_LAUNCH
+  return check_launch(what);
+}
+
 extern "C" int mxf8_lora_down(const void* x, int64_t ldx, const void* a, void* t, int64_t M, int64_t K, int64_t r,
                               hipStream_t stream) {
   if (M < 0 || K <= 0 || r <= 0) return set_error(MXF8_EINVAL, "lora_down: bad shape");
@@ -823,6 +1027,7 @@ extern "C" int mxf8_lora_down(const void* x, int64_t ldx, const void* a, void* t
   // tile, fewer copies of A).  M = 77648 on 256 CUs: 160 rows, 486 tiles in 2 rounds,
   // against 607 tiles of 128 rows in 3.
   const int64_t cus = device_cus();
+  if (cus <= 0) return set_error(MXF8_ELAUNCH, "lora_down: the device's compute-unit count is unavailable");
   int W = 5;
   int64_t best = INT64_MAX;
   for (int w = 5; w >= 2; --w) {

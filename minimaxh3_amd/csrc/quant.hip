@@ -743,6 +743,76 @@ __global__ __launch_bounds__(256) void attn_quant_kv_kernel(const void* __restri
   quant_v_tile<DT, D, VECV>(v, stv, H, S, Sp, sv, v8t, blk, bh, L);
 }
 
+// Fold of the K/V column statistics that the QKV projection's epilogue emits
+// (mxf8_gemm_rowwise_kv_stats: part[stat][p][c], stat 0 key sums, 1 value |max|, over the
+// 128-row blocks p that lie inside one batch item, c = h D + d).  One workgroup per (b, h)
+// and statistic (blockIdx.y: 0 the key mean, 1 the V scales; only the V scales without
+// key_stats).  The blocks of item b are p in
+// [b S / 128, ((b + 1) S - 1) / 128]; the first and the last may hold rows of another item or
+// rows past the end, and for those the item's rows are read from k / v themselves.  Thread t
+// folds channel d = t % D from phase t / D (P = 1024 / D phases): every P-th row of such a
+// block, every P-th clean block (eight loads in flight), in row and block order; the phases
+// are then combined in order.  mean = sum / S, sv = max(amax, 1e-12) / 448 (|max| skips NaN).
+template <int DT, int D>
+__global__ __launch_bounds__(1024) void gemm_kv_stats_fold_kernel(const float* __restrict__ part, int64_t nb,
+                                                                  const void* __restrict__ k, Strides4 stk,
+                                                                  const void* __restrict__ v, Strides4 stv,
+                                                                  int64_t H, int64_t S, int key_stats,
+                                                                  float* __restrict__ mean, float* __restrict__ sv) {
+  constexpr int P = 1024 / D, U = 8, R = 128 / P;
+  constexpr int64_t ES = sizeof(typename Elem<DT>::T);
+  __shared__ float red[P][D];
+  const int64_t bh = blockIdx.x, b = bh / H, h = bh % H, C = H * D;
+  const bool vstat = blockIdx.y != 0 || !key_stats;  // without key statistics: one y index, the V scales
+  const int d = threadIdx.x % D, ph = threadIdx.x / D;
+  const int64_t r0 = b * S, p_lo = r0 / 128, p_hi = (r0 + S - 1) / 128;
+  const float* const src = part + (vstat ? nb * C : 0) + h * D + d;
+  const Strides4& st = vstat ? stv : stk;
+  const typename Elem<DT>::T* const row0 = reinterpret_cast<const typename Elem<DT>::T*>(
+      static_cast<const char*>(vstat ? v : k) + (b * st.b + h * st.h + d * st.d) * ES);
+  float a = 0.0f;
+  auto fold = [&](float x) { a = vstat ? fmaxf(a, fabsf(x)) : a + x; };
+  // rows [s0, s1) of item b (s1 - s0 <= 128), every P-th from this phase: all loads issued
+  // first (clamped indices), then folded in row order
+  auto rows = [&](int64_t s0, int64_t s1) {
+    float x[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) x[u] = Elem<DT>::to_f32(row0[min(s0 + ph + u * P, s1 - 1) * st.s]);
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+      if (s0 + ph + u * P < s1) fold(x[u]);
+  };
+  auto clean = [&](int64_t p) { return p * 128 >= r0 && p * 128 + 128 <= r0 + S; };
+  int64_t pf = p_lo, pl = p_hi;
+  if (!clean(p_lo)) {
+    rows(0, min(p_lo * 128 + 128, r0 + S) - r0);
+    ++pf;
+  }
+  const bool tail = pl >= pf && !clean(pl);
+  if (tail) --pl;
+  for (int64_t p0 = pf + ph; p0 <= pl; p0 += U * P) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = src[min(p0 + u * P, pl) * C];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (p0 + u * P <= pl) {
+        a = vstat ? fmaxf(a, x[u]) : a + x[u];
+      }
+  }
+  if (tail) rows(p_hi * 128 - r0, S);
+  red[ph][d] = a;
+  __syncthreads();
+  if (ph == 0) {
+#pragma unroll
+    for (int j = 1; j < P; ++j) a = vstat ? fmaxf(a, red[j][d]) : a + red[j][d];
+    if (vstat)
+      sv[bh * D + d] = e4m3_scale(a);
+    else
+      mean[bh * D + d] = __fdiv_rn(a, (float)S);
+  }
+}
+
 static bool attn_vec_ok(const void* p, int dtype, const Strides4& st) {
   const int64_t es = dtype == MXF8_F32 ? 4 : 2;
   return st.d == 1 && ((uintptr_t)p % 16 == 0) && ((st.b * es) % 16 == 0) && ((st.h * es) % 16 == 0) &&
@@ -981,6 +1051,26 @@ static void launch_kv(const void* k, const Strides4& stk, bool veck, const void*
 #undef MXF8_KV_CASE
 }
 
+// The quantizing pass of the K/V pair alone (the key mean and V scales given).
+template <int DT, int D>
+static void launch_quant_kv_only(const void* k, const Strides4& stk, bool veck, const void* v, const Strides4& stv,
+                                 bool vecv, int64_t H, int64_t S, int64_t BH, const float* mean, const float* sv,
+                                 uint8_t* k8, float* sk, uint8_t* v8t, hipStream_t stream) {
+  const int64_t nb = cdiv(S, 128);
+  const dim3 qgrid((unsigned)BH, (unsigned)nb);
+#define MXF8_KVQ_CASE(VK, VV)                                                                                    \
+  if (veck == VK && vecv == VV) {                                                                                \
+    attn_quant_kv_kernel<DT, D, VK, VV><<<qgrid, 256, 0, stream>>>(k, stk, v, stv, H, S, nb * 128, mean, sv, k8, \
+                                                                    sk, v8t);                                    \
+    return;                                                                                                      \
+  }
+  MXF8_KVQ_CASE(true, true)
+  MXF8_KVQ_CASE(true, false)
+  MXF8_KVQ_CASE(false, true)
+  MXF8_KVQ_CASE(false, false)
+#undef MXF8_KVQ_CASE
+}
+
 // K and V quantized together: the key mean, the K quantizer, the per-channel V scale and
 // the transposed V quantizer (kernels/fp8_attention.py:338-369) in three launches.
 static int attn_quant_kv_impl(const char* what, const void* k, const int64_t k_strides[4], const void* v,
@@ -1027,6 +1117,47 @@ extern "C" int mxf8_attn_quant_kv(const void* k, const int64_t k_strides[4], con
   float* mean_ws = part + 2 * (int64_t)nch * BH * D;
   return attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
                             mean ? mean : mean_ws, part, nch, stream);
+}
+
+// K and V quantized from the column statistics of the QKV projection that produced them
+// (mxf8_gemm_rowwise_kv_stats): one fold launch for the key mean and the V scales, then the
+// quantizing pass -- K and V are read once.
+extern "C" int mxf8_attn_quant_kv_gemm_stats(const void* k, const int64_t k_strides[4], const void* v,
+                                             const int64_t v_strides[4], int dtype, int64_t B, int64_t H, int64_t S,
+                                             int64_t D, const float* part, int key_stats, uint8_t* k8, float* sk,
+                                             uint8_t* v8t, float* sv, float* mean, hipStream_t stream) {
+  const char* what = "attn_quant_kv_gemm_stats";
+  int rc = attn_quant_kv_checks(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv);
+  if (rc) return rc;
+  if (!part || !mean) return set_error(MXF8_EINVAL, "%s: null statistics or mean", what);
+  if (S < 128) return set_error(MXF8_EINVAL, "%s: S=%lld must be >= 128", what, (long long)S);
+  if ((H * D) % 256) return set_error(MXF8_EINVAL, "%s: H*D must be a multiple of 256", what);
+  if (B * S > (1 << 30)) return set_error(MXF8_EINVAL, "%s: B*S too large", what);
+  const Strides4 stk{k_strides[0], k_strides[1], k_strides[2], k_strides[3]};
+  const Strides4 stv{v_strides[0], v_strides[1], v_strides[2], v_strides[3]};
+  const bool veck = attn_vec_ok(k, dtype, stk), vecv = attn_vec_ok(v, dtype, stv);
+  const int64_t BH = B * H, nb = cdiv(B * S, 128);
+  // grid y: the key mean (only when it comes from part) and the V scales
+  const dim3 fgrid((unsigned)BH, key_stats ? 2u : 1u);
+#define MXF8_FOLD(DT_, D_)                                                                                         \
+  gemm_kv_stats_fold_kernel<DT_, D_><<<fgrid, 1024, 0, stream>>>(part, nb, k, stk, v, stv, H, S, key_stats, mean, \
+                                                                  sv)
+  if (dtype == MXF8_BF16) {
+    if (D == 128) MXF8_FOLD(MXF8_BF16, 128); else MXF8_FOLD(MXF8_BF16, 64);
+  } else {
+    if (D == 128) MXF8_FOLD(MXF8_F16, 128); else MXF8_FOLD(MXF8_F16, 64);
+  }
+#undef MXF8_FOLD
+  rc = check_launch("attn_quant_kv_gemm_stats(fold)");
+  if (rc) return rc;
+  if (dtype == MXF8_BF16) {
+    if (D == 128) launch_quant_kv_only<MXF8_BF16, 128>(k, stk, veck, v, stv, vecv, H, S, BH, mean, sv, k8, sk, v8t, stream);
+    else launch_quant_kv_only<MXF8_BF16, 64>(k, stk, veck, v, stv, vecv, H, S, BH, mean, sv, k8, sk, v8t, stream);
+  } else {
+    if (D == 128) launch_quant_kv_only<MXF8_F16, 128>(k, stk, veck, v, stv, vecv, H, S, BH, mean, sv, k8, sk, v8t, stream);
+    else launch_quant_kv_only<MXF8_F16, 64>(k, stk, veck, v, stv, vecv, H, S, BH, mean, sv, k8, sk, v8t, stream);
+  }
+  return check_launch(what);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -12,6 +12,8 @@ q's strides, fp8_attention.py:296 and 379, which is only right for contiguous q)
 """
 from __future__ import annotations
 
+from typing import NamedTuple
+
 import torch
 
 from .. import ops
@@ -60,6 +62,15 @@ def is_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
 fuse_q_quant = True
 
 
+class KVStats(NamedTuple):
+    """Column statistics of k and v from the QKV projection that produced them
+    (``FP8Linear.forward_qkv``): ``part`` [2, ceil(B S / 128), H D] fp32 (key sums, value
+    |max|), ``key`` False when only the value statistics are present."""
+
+    part: torch.Tensor
+    key: bool = True
+
+
 def fp8_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -68,19 +79,26 @@ def fp8_attention(
     key_mask: torch.Tensor | None = None,
     key_bias: torch.Tensor | None = None,
     repair_tau: float = -1.0,
+    kv_stats: KVStats | None = None,
 ) -> torch.Tensor:
     """Non-causal FP8 attention over [B, H, S, D] tensors (fp8_attention.py:300-403).
 
     key_mask: bool [B, Sk] (True = attend) or None; key_bias: float [B, Sk] additive
     (natural log) bias or None, entries <= -1e8 mask the key; repair_tau < 0 disables the
     exact repair of large probabilities.  Returns [B, H, Sq, D] in q's dtype.
+    kv_stats (an extension): the statistics ``FP8Linear.forward_qkv`` returned with the
+    projection that k and v are views of; the K/V quantizers then read k and v once.
     """
     if not is_supported(q, k, v):
         raise ValueError("Unsupported inputs for fp8_attention")
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     c = ops.softmax_c(scale, D)
-    k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
+    if kv_stats is None:
+        k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
+    else:
+        mean = None if kv_stats.key else ops.attn_kmean(k)
+        k8, sk, v8t, sv, _ = ops.attn_quant_kv_gemm_stats(k, v, kv_stats.part, mean)
     if fuse_q_quant and ops.attn_fwd_q_supported(q):
         # the attention kernel quantizes Q itself (same codes and scales as attn_quant_q)
         return ops.attn_fwd_q(q, c, k8, v8t, sk, sv, key_mask, key_bias, float(repair_tau), Sk)

@@ -195,10 +195,11 @@ class FP8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape
         x2d = x.reshape(-1, self.in_features)
-        if self.adapters and x.dtype != torch.bfloat16:
+        if x.dtype != torch.bfloat16 and (self.adapters or self.act == ACT_GELU_TANH):
             # The reference converts the bf16 linear output to x's dtype and adds each LoRA
-            # branch in that dtype (fp8_linear.py:105-108); the fused epilogue adds in bf16,
-            # so other dtypes take the reference's sequence (then the folded tanh-GELU).
+            # branch in that dtype (fp8_linear.py:105-108), and the FFN's tanh-GELU module
+            # then acts in that dtype; the fused epilogue adds and rounds in bf16, so other
+            # dtypes take the reference's sequence.
             x8, x_scale = quantize_rows(x2d)
             out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, ACT_NONE, None, None, 0.0)
             out = apply_lora_adapters(x2d, out.to(x.dtype), self.adapters)
@@ -210,6 +211,35 @@ class FP8Linear(nn.Module):
         out = ops.gemm_rowwise(x8, self.w8, x_scale, self.w_scale, self.bias, int(self.act), lora_t, lora_b,
                                lora_scale)
         return out.reshape(*orig_shape[:-1], self.out_features).to(x.dtype)
+
+    def forward_qkv(self, x: torch.Tensor, heads: int, head_dim: int, key_stats: bool = True):
+        """``forward`` of a fused QKV projection -- x [B, S, in] -> [B, S, 3 heads head_dim] with
+        the q, k and v parts in that order, each head-major -- that also returns the column
+        statistics its attention's K/V quantizers need (an extension with no counterpart in the
+        reference; they replace the key mean and the V-scale pass of kernels/fp8_attention.py:
+        338 and 140-155).  Returns (out, stats): pass stats as ``fp8_attention(..., kv_stats=)``
+        with k and v the [B, H, S, D] views of out's k and v parts, and K and V are read once.
+        With ``key_stats=False`` only the V statistics are taken (keys that are transformed
+        after the projection, e.g. by a per-head norm or RoPE, need their own mean).
+
+        The output equals ``forward(x)`` bit for bit.  Where the statistics epilogue does not
+        apply (LoRA adapters or an activation on this module, a non-bf16 input, S < 128, or
+        heads x head_dim not a multiple of 256) stats is None, which ``fp8_attention`` takes
+        as "compute the statistics from k and v"."""
+        if x.ndim != 3 or x.shape[2] != self.in_features:
+            raise ValueError(f"forward_qkv: expected x [B, S, {self.in_features}]")
+        B, S, _ = x.shape
+        C = int(heads) * int(head_dim)
+        if self.out_features != 3 * C:
+            raise ValueError(f"forward_qkv: out_features {self.out_features} != 3 x {heads} x {head_dim}")
+        if self.adapters or self.act != ACT_NONE or x.dtype != torch.bfloat16 or S < 128 or C % 256:
+            return self.forward(x), None
+        x8, x_scale = quantize_rows(x.reshape(-1, self.in_features))
+        out, part = ops.gemm_rowwise_kv_stats(x8, self.w8, x_scale, self.w_scale, self.bias, S,
+                                              C if key_stats else -1, 2 * C, C)
+        from .fp8_attention import KVStats
+
+        return out.reshape(B, S, self.out_features), KVStats(part, bool(key_stats))
 
     def forward_adaln(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6,
                       eager_rounding: bool = False) -> torch.Tensor:

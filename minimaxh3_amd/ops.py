@@ -169,6 +169,52 @@ def _(a8, w8, sa, sw, bias, act, lora_t, lora_b, lora_scale):
     return a8.new_empty((a8.shape[0], w8.shape[0]), dtype=torch.bfloat16)
 
 
+def kv_stats_shape(M: int, C: int) -> tuple[int, int, int]:
+    """Shape of the K/V column statistics of gemm_rowwise_kv_stats: [2, ceil(M/128), C]
+    (key sums, value |max|; 128-row block; column)."""
+    return (2, _cdiv(M, 128), C)
+
+
+@torch.library.custom_op("mxf8::gemm_rowwise_kv_stats", mutates_args=())
+def gemm_rowwise_kv_stats(a8: torch.Tensor, w8: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor,
+                          bias: torch.Tensor | None, seq_len: int, k_col0: int, v_col0: int,
+                          cols: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """gemm_rowwise (no LoRA, no activation) of a fused QKV projection, plus the column
+    statistics its attention's K/V quantizers need: per-channel sums of the key columns
+    [k_col0, k_col0 + cols) and |max| of the value columns [v_col0, v_col0 + cols) (-1: none)
+    over each batch item's seq_len rows (kernels/fp8_attention.py:338, 140-155).  Returns
+    (out [M, N] bf16, equal to gemm_rowwise's bit for bit, stats [2, ceil(M/128), cols]: the
+    statistic of every 128-row block inside one batch item; the other blocks' entries are
+    not written)."""
+    _prep(a8, "gemm_rowwise_kv_stats")
+    M, K = a8.shape
+    Nn = w8.shape[0]
+    if a8.dtype != E4M3 or w8.dtype != E4M3 or w8.dim() != 2 or w8.shape[1] != K:
+        raise ValueError("gemm_rowwise_kv_stats: e4m3 a8 [M, K] and w8 [N, K] expected")
+    if not (a8.is_contiguous() and w8.is_contiguous() and sa.is_contiguous() and sw.is_contiguous()):
+        raise ValueError("gemm_rowwise_kv_stats: operands must be contiguous")
+    if sa.dtype != torch.float32 or sa.numel() != M or sw.dtype != torch.float32 or sw.numel() != Nn:
+        raise ValueError(f"gemm_rowwise_kv_stats: fp32 scales of {M} rows and {Nn} channels expected")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != Nn or not bias.is_contiguous()):
+        raise ValueError(f"gemm_rowwise_kv_stats: bias must be {Nn} contiguous bf16 values")
+    for t, name in ((w8, "w8"), (sa, "sa"), (sw, "sw"), (bias, "bias")):
+        _on(t, a8.device, f"gemm_rowwise_kv_stats: {name}")
+    out = torch.empty((M, Nn), dtype=torch.bfloat16, device=a8.device)
+    stats = torch.empty(kv_stats_shape(M, cols), dtype=torch.float32, device=a8.device)
+    with torch.cuda.device(a8.device):
+        N.check(N.load().mxf8_gemm_rowwise_kv_stats(
+            a8.data_ptr(), w8.data_ptr(), sa.data_ptr(), sw.data_ptr(), N.ptr(bias), out.data_ptr(), M, Nn, K, Nn,
+            int(seq_len), int(k_col0), int(v_col0), int(cols), stats.data_ptr(), N.stream_of(a8)),
+            "gemm_rowwise_kv_stats")
+    return out, stats
+
+
+@gemm_rowwise_kv_stats.register_fake
+def _(a8, w8, sa, sw, bias, seq_len, k_col0, v_col0, cols):
+    return (a8.new_empty((a8.shape[0], w8.shape[0]), dtype=torch.bfloat16),
+            a8.new_empty(kv_stats_shape(a8.shape[0], cols), dtype=torch.float32))
+
+
 @torch.library.custom_op("mxf8::lora_down", mutates_args=())
 def lora_down(x: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
     """t = bf16(x A^T): x [M, K] bf16, A [r, K] bf16 -> [M, r] bf16 (kernels/fp8_linear.py:53)."""
@@ -313,6 +359,53 @@ def attn_quant_kv(k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch
 
 @attn_quant_kv.register_fake
 def _(k, v):
+    B, H, S, D = k.shape
+    nk = _cdiv(S, 128)
+    f32 = torch.float32
+    return (k.new_empty((B, H, nk * 128, D), dtype=E4M3), k.new_empty((B, H, nk), dtype=f32),
+            k.new_empty((B, H, D, nk * 128), dtype=E4M3), k.new_empty((B, H, D), dtype=f32),
+            k.new_empty((B, H, D), dtype=f32))
+
+
+@torch.library.custom_op("mxf8::attn_quant_kv_gemm_stats", mutates_args=())
+def attn_quant_kv_gemm_stats(k: torch.Tensor, v: torch.Tensor, stats: torch.Tensor,
+                             key_mean: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                     torch.Tensor, torch.Tensor]:
+    """attn_quant_kv for k, v [B, H, S, D] that are views of a gemm_rowwise_kv_stats output,
+    from its statistics: one fold launch and one quantizing pass (K and V read once).  With
+    ``key_mean`` [B, H, D] fp32 given, the key mean is that (e.g. of keys transformed after
+    the projection) and only the V statistics come from ``stats``.  Same outputs as
+    attn_quant_kv: (K8, sk, V8T, sv, key mean)."""
+    _prep(k, "attn_quant_kv_gemm_stats")
+    if k.shape != v.shape or k.dtype != v.dtype or k.device != v.device:
+        raise ValueError("attn_quant_kv_gemm_stats: k and v must have one shape, dtype and device")
+    B, H, S, D = k.shape
+    _on(stats, k.device, "attn_quant_kv_gemm_stats: stats")
+    if stats.dtype != torch.float32 or tuple(stats.shape) != kv_stats_shape(B * S, H * D) or not stats.is_contiguous():
+        raise ValueError(f"attn_quant_kv_gemm_stats: stats must be contiguous fp32 {kv_stats_shape(B * S, H * D)}, "
+                         f"got {stats.dtype} {tuple(stats.shape)}")
+    nk = _cdiv(S, 128)
+    k8 = torch.empty((B, H, nk * 128, D), dtype=E4M3, device=k.device)
+    sk = torch.empty((B, H, nk), dtype=torch.float32, device=k.device)
+    v8t = torch.empty((B, H, D, nk * 128), dtype=E4M3, device=k.device)
+    sv = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
+    if key_mean is None:
+        mean = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
+    else:
+        _on(key_mean, k.device, "attn_quant_kv_gemm_stats: key_mean")
+        if key_mean.numel() != B * H * D:
+            raise ValueError(f"attn_quant_kv_gemm_stats: key_mean must hold B*H*D = {B * H * D} values")
+        mean = key_mean.to(torch.float32).reshape(B, H, D).clone()
+    with torch.cuda.device(k.device):
+        N.check(N.load().mxf8_attn_quant_kv_gemm_stats(
+            k.data_ptr(), N.strides4(k), v.data_ptr(), N.strides4(v), N.dtype_code(k.dtype), B, H, S, D,
+            stats.data_ptr(), int(key_mean is None), k8.data_ptr(), sk.data_ptr(), v8t.data_ptr(), sv.data_ptr(),
+            mean.data_ptr(), N.stream_of(k)), "attn_quant_kv_gemm_stats")
+    return k8, sk, v8t, sv, mean
+
+
+@attn_quant_kv_gemm_stats.register_fake
+def _(k, v, stats, key_mean):
     B, H, S, D = k.shape
     nk = _cdiv(S, 128)
     f32 = torch.float32

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(N.lib_path())
     for name in _declared():
         assert hasattr(raw, name), name
-    assert lib.mxf8_abi_version() == 200
+    assert lib.mxf8_abi_version() == 201
     assert lib.mxf8_last_error() is not None
 
 
@@ -120,3 +120,29 @@ def test_attention_argument_checks(lib):
     assert lib.mxf8_attn_quant_kv(d, st, d, st, 0, 1, 1, 0, 128, d, d, d, d, None, d, None) == 1
     assert lib.mxf8_attn_kv_workspace_bytes(1, 24, 20280, 128) > 0
     assert lib.mxf8_attn_kv_workspace_bytes(1, 0, 20280, 128) == 0
+
+
+def test_kv_stats_argument_checks(lib):
+    d = ctypes.c_void_p(256)
+    args = lambda M=600, N=768, K=256, ld=768, S=300, kc=256, vc=512, C=256, part=d: (
+        d, d, d, d, None, d, M, N, K, ld, S, kc, vc, C, part, None)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(N=640, ld=640)) == 1 and "multiples of 256" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(S=64, M=640)) == 1 and "S=64" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(S=250)) == 1 and "divide" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(C=128)) == 1 and "C=128" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(kc=-1, vc=-1)) == 1 and "neither" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(vc=640)) == 1 and "column range" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(kc=256, vc=256)) == 1 and "overlap" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(part=None)) == 1 and "null" in _err(lib)
+    assert lib.mxf8_gemm_rowwise_kv_stats(*args(K=24)) == 1 and "multiple of 16" in _err(lib)
+    assert lib.mxf8_gemm_kv_stats_bytes(20280, 3072) == 2 * 159 * 3072 * 4
+    assert lib.mxf8_gemm_kv_stats_bytes(0, 3072) == 0
+    st = N._I64x4(1, 1, 1, 1)
+    assert lib.mxf8_attn_quant_kv_gemm_stats(d, st, d, st, 0, 1, 2, 100, 128, d, 1, d, d, d, d, d, None) == 1 \
+        and "S=100" in _err(lib)
+    assert lib.mxf8_attn_quant_kv_gemm_stats(d, st, d, st, 0, 1, 1, 300, 128, d, 1, d, d, d, d, d, None) == 1 \
+        and "H*D" in _err(lib)
+    assert lib.mxf8_attn_quant_kv_gemm_stats(d, st, d, st, 0, 1, 2, 300, 128, None, 1, d, d, d, d, d, None) == 1 \
+        and "null" in _err(lib)
+    assert lib.mxf8_attn_quant_kv_gemm_stats(d, st, d, st, 0, 1, 2, 300, 96, d, 1, d, d, d, d, d, None) == 1 \
+        and "D must be" in _err(lib)

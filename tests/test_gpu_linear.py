@@ -615,3 +615,16 @@ def test_fp16_input_lora_follows_reference_sequence(fl, gelu):
     assert_gemm_close(out.float().cpu().numpy(), ref)
     no_lora = ol.fp8_linear_forward(x, w8c, swc, b, gelu=gelu, in_dtype="fp16")
     assert np.abs(ref - no_lora).max() > 5e-2 * np.abs(ref).max()
+    # without adapters an fp16 input with the folded GELU also takes the reference's sequence
+    # (bf16 linear output -> fp16 -> GELU in fp16), bit for bit against the same launches
+    mod.adapters.clear()
+    out = mod(to_gpu(x, torch.float16))
+    torch.cuda.synchronize()
+    assert_gemm_close(out.float().cpu().numpy(), no_lora)
+    if gelu:
+        from minimaxh3_amd import ops
+        x16 = to_gpu(x, torch.float16)
+        x8g, sag = fl.quantize_rows(x16)
+        lin_out = ops.gemm_rowwise(x8g, mod.w8, sag, mod.w_scale, mod.bias, 0, None, None, 0.0).to(torch.float16)
+        seq = torch.nn.functional.gelu(lin_out, approximate="tanh")
+        assert torch.equal(out.view(torch.int16), seq.view(torch.int16))

@@ -22,7 +22,7 @@ def _packed_kv(B, H, S, D, seed):
     return kv[:, :, 0].permute(0, 2, 1, 3), kv[:, :, 1].permute(0, 2, 1, 3)
 
 
-def _noalloc(k, v):
+def _noalloc(k, v, with_mean=True):
     from minimaxh3_amd import _native as N
     B, H, S, D = k.shape
     nk = -(-S // 128)
@@ -33,7 +33,7 @@ def _noalloc(k, v):
     mean = torch.empty((B, H, D), dtype=torch.float32, device=k.device)
     rc = N.load().mxf8_attn_quant_kv_noalloc(
         k.data_ptr(), N.strides4(k), v.data_ptr(), N.strides4(v), N.dtype_code(k.dtype), B, H, S, D, k8.data_ptr(),
-        sk.data_ptr(), v8t.data_ptr(), sv.data_ptr(), mean.data_ptr(), N.stream_of(k))
+        sk.data_ptr(), v8t.data_ptr(), sv.data_ptr(), mean.data_ptr() if with_mean else None, N.stream_of(k))
     N.check(rc, "attn_quant_kv_noalloc")
     return k8, sk, v8t, sv, mean
 
@@ -51,6 +51,14 @@ def test_noalloc_equals_workspace_entry_point_twice(first, second):
             if r.dtype == torch.float8_e4m3fn:
                 r, o = r.view(torch.uint8), o.view(torch.uint8)
             assert torch.equal(r, o), (shape, name)
+        # without a mean buffer the key mean lives in the scratch array after the partial slabs
+        # (stale from the call before): the codes and scales must not change
+        got = _noalloc(k, v, with_mean=False)
+        torch.cuda.synchronize()
+        for name, r, o in zip(("k8", "sk", "v8t", "sv"), ref[:4], got[:4]):
+            if r.dtype == torch.float8_e4m3fn:
+                r, o = r.view(torch.uint8), o.view(torch.uint8)
+            assert torch.equal(r, o), (shape, name, "mean=NULL")
 
 
 def test_noalloc_rejects_shapes_beyond_its_scratch():

@@ -747,19 +747,19 @@ __global__ __launch_bounds__(256) void attn_quant_kv_kernel(const void* __restri
 // (mxf8_gemm_rowwise_kv_stats: part[stat][p][c], stat 0 key sums, 1 value |max|, over the
 // 128-row blocks p that lie inside one batch item, c = h D + d).  One workgroup per (b, h)
 // and statistic (blockIdx.y: 0 the key mean, 1 the V scales; only the V scales without
-// key_stats).  The blocks of item b are p in
-// [b S / 128, ((b + 1) S - 1) / 128]; the first and the last may hold rows of another item or
-// rows past the end, and for those the item's rows are read from k / v themselves.  Thread t
-// folds channel d = t % D from phase t / D (P = 1024 / D phases): every P-th row of such a
-// block, every P-th clean block (eight loads in flight), in row and block order; the phases
-// are then combined in order.  mean = sum / S, sv = max(amax, 1e-12) / 448 (|max| skips NaN).
+// key_stats).  The blocks of item b are p in [b S / 128, ((b + 1) S - 1) / 128]; the first
+// and the last may hold rows of another item or rows past the end, and for those the item's
+// rows are read from k / v themselves.  Thread t folds channel d = t % D from phase t / D
+// (P = 1024 / D phases): every P-th row of such a block and every P-th clean block (24 loads
+// in flight: one round for a 480p item), in row and block order; the phases are then
+// combined in order.  mean = sum / S, sv = max(amax, 1e-12) / 448 (|max| skips NaN).
 template <int DT, int D>
 __global__ __launch_bounds__(1024) void gemm_kv_stats_fold_kernel(const float* __restrict__ part, int64_t nb,
                                                                   const void* __restrict__ k, Strides4 stk,
                                                                   const void* __restrict__ v, Strides4 stv,
                                                                   int64_t H, int64_t S, int key_stats,
                                                                   float* __restrict__ mean, float* __restrict__ sv) {
-  constexpr int P = 1024 / D, U = 8, R = 128 / P;
+  constexpr int P = 1024 / D, U = 24, R = 128 / P;
   constexpr int64_t ES = sizeof(typename Elem<DT>::T);
   __shared__ float red[P][D];
   const int64_t bh = blockIdx.x, b = bh / H, h = bh % H, C = H * D;

@@ -513,9 +513,11 @@ def summarize_counters(directories: list[str]) -> str:
     if fetch_k and write_k:
         lines += [f"Calibration (the 1 GiB bf16 negation reads and writes exactly 1 GiB per launch): bytes read = "
                   f"{fetch_k:.3f} x FETCH_SIZE KiB x 1024, bytes written = {write_k:.3f} x WRITE_SIZE KiB x 1024.", ""]
+    lds_cols = any(m(p, "SQ_LDS_IDX_ACTIVE") is not None for p in per)
     lines += ["| part | kernel cycles (M) | clock GHz | MFMA busy | VALU busy | MFMA+VALU co-issue | LDS busy | wait | "
-              "VALU instr / MFMA instr | HBM read MB | HBM write MB |",
-              "|---|---|---|---|---|---|---|---|---|---|---|"]
+              "VALU instr / MFMA instr | HBM read MB | HBM write MB |" +
+              (" LDS active | LDS data FIFO full |" if lds_cols else ""),
+              "|---|---|---|---|---|---|---|---|---|---|---|" + ("---|---|" if lds_cols else "")]
     for p in PART_ORDER:
         if p not in per:
             continue
@@ -535,13 +537,19 @@ def summarize_counters(directories: list[str]) -> str:
         wr = f"{m(p, 'WRITE_SIZE') * 1024 * write_k / 1e6:.1f}" if m(p, "WRITE_SIZE") is not None and write_k else "-"
         dur = m(p, "duration_ns")
         ghz = f"{cyc / dur:.2f}" if cyc and dur else "-"
+        extra = ""
+        if lds_cols:
+            # per-CU cycles (summed over the 256 CUs) over the kernel's cycles
+            extra = f" {frac('SQ_LDS_IDX_ACTIVE', 4.0)} | {frac('SQ_LDS_DATA_FIFO_FULL', 4.0)} |"
         lines.append(f"| `{p}` | {cyc / 1e6:.2f} | {ghz} | {frac('SQ_VALU_MFMA_BUSY_CYCLES')} | "
                      f"{frac('SQ_ACTIVE_INST_VALU', 4.0)} | {frac('SQ_VALU_MFMA_COEXEC_CYCLES')} | "
-                     f"{frac('SQ_ACTIVE_INST_LDS', 4.0)} | {wait} | {ratio} | {rd} | {wr} |"
-                     if cyc else f"| `{p}` | - | - | - | - | - | - | - | {ratio} | {rd} | {wr} |")
+                     f"{frac('SQ_ACTIVE_INST_LDS', 4.0)} | {wait} | {ratio} | {rd} | {wr} |{extra}"
+                     if cyc else f"| `{p}` | - | - | - | - | - | - | - | {ratio} | {rd} | {wr} |{extra}")
     lines += ["", "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles); VALU busy = 4 x "
                   "SQ_ACTIVE_INST_VALU (quad-cycles) / the same; co-issue = SQ_VALU_MFMA_COEXEC_CYCLES / the same; "
-                  "LDS busy = 4 x SQ_ACTIVE_INST_LDS / the same; kernel cycles = SQ_BUSY_CYCLES / 32; clock = "
+                  "LDS busy = 4 x SQ_ACTIVE_INST_LDS / the same; LDS active = SQ_LDS_IDX_ACTIVE (cycles the LDS "
+                  "serves indexed accesses, summed over the CUs) / (256 CUs x kernel cycles), FIFO full = "
+                  "SQ_LDS_DATA_FIFO_FULL over the same; kernel cycles = SQ_BUSY_CYCLES / 32; clock = "
                   "kernel cycles / the dispatch's duration in the same pass (the 5.0 PFLOP/s peak assumes 2.4 GHz); "
                   "wait = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."]
     return "\n".join(lines)

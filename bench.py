@@ -30,7 +30,9 @@ value = algorithmic FLOPs of the step (2*M*N*K per GEMM with the un-padded M,
 time of the step, in TFLOP/s, with every input resident in HBM before the timed region.
 In the timed steps only the attention launches are bracketed by HIP events on the stream
 they run on (the largest gives the roofline entry); the per-kernel breakdown comes from
-the same number of steps run again after the timed ones with every launch bracketed.  The CPU baseline times the
+the same number of steps run again after the timed ones with every launch bracketed (for
+--workload linear2048, whose timed steps are one replay of a HIP graph holding all of them,
+from a graph of 20 copies of each launch, timed by one event pair around its replay).  The CPU baseline times the
 reference's torch CPU fallbacks (fp32 dequant-matmul and SDPA) on a bounded sample and
 scales those rates to the step's FLOP mix.
 
@@ -92,8 +94,9 @@ WORKLOADS = {
 # channels are scaled x20
 LINEAR_SETS = {"linear2048": (("linear", HIDDEN, HIDDEN, 0),)}
 NO_OUTLIERS = ("linear2048",)
-# workloads whose step is captured once in a HIP graph and replayed: two launches of ~20 us,
-# which Python launches one by one would not keep the GPU busy with
+# workloads whose K timed steps are captured in one HIP graph and replayed once: a step is two
+# launches of ~5 and ~24 us, which neither Python launches nor a graph replay per step keep
+# the GPU busy with
 GRAPHED = ("linear2048",)
 
 
@@ -162,30 +165,56 @@ def build_workload(torch, dev, tokens: int, lora_rank: int, attns, adaln: bool =
 
 class Timers:
     """Per-kernel HIP event pairs recorded on the launching (current) stream; with `prefix`,
-    only the launches whose part name starts with it are bracketed."""
+    only the launches whose part name starts with it are timed.
 
-    def __init__(self, torch, prefix: str = ""):
+    reps = 0 brackets each launch in the step with an event pair.  reps > 0 (graph-replayed
+    workloads, whose launches take ~20 us) keeps the first launch of each part and, in
+    graph_times(), captures `reps` copies of it in a HIP graph of its own and times one
+    replay with one event pair: an event pair around a single short launch from Python
+    measures the host's launch gap, not the kernel."""
+
+    def __init__(self, torch, prefix: str = "", reps: int = 0):
         self.torch = torch
         self.prefix = prefix
+        self.reps = reps
         self.pairs: dict[str, list] = {}
+        self.launches: dict[str, tuple] = {}
 
-    def start(self, name):
+    def run(self, name, fn, *args):
         if not name.startswith(self.prefix):
-            return None
-        e = self.torch.cuda.Event(enable_timing=True)
-        e.record()
-        return name, e
-
-    def stop(self, tok):
-        if tok is None:
-            return
-        name, s = tok
+            return fn(*args)
+        if self.reps:
+            self.launches.setdefault(name, (fn, args))
+            return fn(*args)
+        s = self.torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn(*args)
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
         self.pairs.setdefault(name, []).append((s, e))
+        return out
+
+    def graph_times(self):
+        torch = self.torch
+        for name, (fn, args) in self.launches.items():
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(self.reps):
+                    fn(*args)
+            g.replay()
+            torch.cuda.synchronize()
+            for _ in range(3):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                g.replay()
+                e.record()
+                self.pairs.setdefault(name, []).append((s, e))
+            torch.cuda.synchronize()
+            del g
 
     def mean_ms(self):
-        return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
+        n = max(self.reps, 1)
+        return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) / n for k, v in self.pairs.items()}
 
 
 def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bool = True, tau: float = -1.0,
@@ -199,56 +228,41 @@ def run_step(torch, ops, linears, attn_inputs, timers: Timers | None, fuse_q: bo
     the K/V statistics from the projection's epilogue ("stats": gemm_rowwise_kv_stats +
     attn_quant_kv_gemm_stats, K and V read once) or from their own pass ("pass":
     attn_quant_kv)."""
-    tick = timers.start if timers else (lambda n: None)
-    tock = timers.stop if timers else (lambda t: None)
+    timed = timers.run if timers else (lambda name, fn, *args: fn(*args))
     outs = []
 
     def attention(name, q, k, v, mask, part=None):
         sfx = "" if name == "attn" else f"[{name}]"
         c = ops.softmax_c(None, HEAD_DIM)
-        t = tick("attn_quant_kv" + sfx)
         if part is None:
-            k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
+            k8, sk, v8t, sv, _ = timed("attn_quant_kv" + sfx, ops.attn_quant_kv, k, v)
         else:
-            k8, sk, v8t, sv, _ = ops.attn_quant_kv_gemm_stats(k, v, part, None)
-        tock(t)
+            k8, sk, v8t, sv, _ = timed("attn_quant_kv" + sfx, ops.attn_quant_kv_gemm_stats, k, v, part, None)
         if fuse_q:
             # the Q quantizer runs inside the attention launch
-            t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd_q(q, c, k8, v8t, sk, sv, mask, None, tau, k.shape[2]))
-            tock(t)
+            outs.append(timed("attn_fwd" + sfx, ops.attn_fwd_q, q, c, k8, v8t, sk, sv, mask, None, tau,
+                              k.shape[2]))
         else:
-            t = tick("attn_quant_q" + sfx)
-            q8, sq = ops.attn_quant_q(q, c)
-            tock(t)
-            t = tick("attn_fwd" + sfx)
-            outs.append(ops.attn_fwd(q8, k8, v8t, sq, sk, sv, mask, None, tau, q, k.shape[2]))
-            tock(t)
+            q8, sq = timed("attn_quant_q" + sfx, ops.attn_quant_q, q, c)
+            outs.append(timed("attn_fwd" + sfx, ops.attn_fwd, q8, k8, v8t, sq, sk, sv, mask, None, tau, q,
+                              k.shape[2]))
 
     for name, mod, x, mod_params in linears:
         if mod_params is None:
-            t = tick(f"quant_rows[{name}]")
-            x8, sa = ops.quant_rows(x)
-            tock(t)
+            x8, sa = timed(f"quant_rows[{name}]", ops.quant_rows, x)
         else:
             # x is the block's hidden state; the linear's input is its adaLN modulation
-            t = tick(f"adaln_quant[{name}]")
-            x8, sa, y = ops.adaln_quant_rows(x.unsqueeze(0), mod_params[0], mod_params[1], 1e-6, False,
-                                             bool(mod.adapters))
-            tock(t)
-            x = y
+            x8, sa, x = timed(f"adaln_quant[{name}]", ops.adaln_quant_rows, x.unsqueeze(0), mod_params[0],
+                              mod_params[1], 1e-6, False, bool(mod.adapters))
         lt, lb, ls = None, None, 0.0
         if mod.adapters:
-            t = tick(f"lora_down[{name}]")
-            lt, lb, ls = mod._lora_operands(x)
-            tock(t)
-        t = tick(f"gemm[{name}]")
+            lt, lb, ls = timed(f"lora_down[{name}]", mod._lora_operands, x)
         if chain == "stats" and name == "qkv":
-            out, part = ops.gemm_rowwise_kv_stats(x8, mod.w8, sa, mod.w_scale, mod.bias, x.shape[0], HIDDEN,
-                                                  2 * HIDDEN, HIDDEN)
+            out, part = timed(f"gemm[{name}]", ops.gemm_rowwise_kv_stats, x8, mod.w8, sa, mod.w_scale, mod.bias,
+                              x.shape[0], HIDDEN, 2 * HIDDEN, HIDDEN)
         else:
-            out, part = ops.gemm_rowwise(x8, mod.w8, sa, mod.w_scale, mod.bias, int(mod.act), lt, lb, ls), None
-        tock(t)
+            out, part = timed(f"gemm[{name}]", ops.gemm_rowwise, x8, mod.w8, sa, mod.w_scale, mod.bias,
+                              int(mod.act), lt, lb, ls), None
         outs.append(out)
         if chain and name == "qkv":
             (aname, q, k, v, mask), = attn_inputs
@@ -626,7 +640,8 @@ def main() -> int:
         torch.cuda.synchronize()
         graph = None
         if graphed:
-            # one step captured on a side stream, replayed as one launch per step
+            # the K timed steps captured back to back in one graph (after one eager step on a
+            # side stream), replayed once untimed, then once in the timed region
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
@@ -634,29 +649,36 @@ def main() -> int:
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                step()
-            for _ in range(args.warmup):
-                graph.replay()
+                for _ in range(args.steps):
+                    step()
+            graph.replay()
             torch.cuda.synchronize()
-        log(f"[bench] warmup done ({args.warmup} steps{', then a captured step replayed as often' if graphed else ''})")
+        log(f"[bench] warmup done ({args.warmup} steps{f', then the {args.steps} captured steps replayed once' if graphed else ''})")
         # The timed steps bracket only the attention launches (the roofline kernel) with HIP
         # events: an event pair around every launch adds ~0.1 ms to a 5 ms step.
         roof_timers = Timers(torch, prefix="attn_fwd")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(args.steps):
-            if graph is not None:
-                graph.replay()
-            else:
+        if graph is not None:
+            graph.replay()  # the K steps
+        else:
+            for _ in range(args.steps):
                 step(roof_timers)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         log(f"[bench] timed {args.steps} steps in {elapsed:.3f} s")
-        # per-launch breakdown: the same steps again, every launch bracketed (not timed)
-        timers = Timers(torch)
-        for _ in range(args.steps):
+        # per-launch breakdown (not timed): the same steps again with every launch bracketed,
+        # or, for a graph-replayed step, each launch timed over a graph of 20 copies of it
+        if graphed:
+            timers = Timers(torch, reps=20)
             step(timers)
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            timers.graph_times()
+        else:
+            timers = Timers(torch)
+            for _ in range(args.steps):
+                step(timers)
+            torch.cuda.synchronize()
     ms_step = elapsed * 1e3 / args.steps
     kern = timers.mean_ms()
     roof_kern = roof_timers.mean_ms()
@@ -719,7 +741,7 @@ def main() -> int:
         roof_name, roof_f, roof_t = biggest
         roof_kernel = f"{roof_name}: attn_fwd_kernel<128,...>"
     else:
-        # no attention in the step: the largest GEMM (its per-launch event time)
+        # no attention in the step: the largest GEMM (its per-launch time from the breakdown)
         roof_name, roof_f, roof_t = biggest_gemm
         roof_kernel = f"{roof_name}: gemm_fp8_rowwise_kernel"
     achieved = roof_f / (roof_t * 1e-3) / 1e12

@@ -39,6 +39,8 @@
 // fragments three products ahead.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace mxf8 {
@@ -83,6 +85,43 @@ struct AttnQ16 {
   float c;        // softmax scale * log2(e)
   float* sq_out;  // [B, H, ceil(Sq / 128)] or null
 };
+
+// The Q block maximum of one 4-wave group, exchanged through LDS without a workgroup
+// barrier (attn_fwd_resident_kernel): wave w of the group writes its maximum of round n to
+// val[n & 1][w] and then n to tag[w]; a wave reads the four maxima once every tag has
+// reached n.  A wave's LDS accesses take effect in issue order, so a tag never runs ahead
+// of its value.  A value slot is written again at round n + 2, which its writer reaches only
+// after the round n + 1 tags of all four waves, each written after that wave's round n read.
+struct AttnGroupX {
+  int tag[4];
+  float val[2][4];
+};
+
+// Rounds a wave polls the tags before it gives up and goes on with the values it sees
+// (with s_sleep 1, about 64 cycles each: some 0.2 s).  The four waves of a group go through
+// the same rounds, so this bound is never reached; it keeps a wave from spinning forever.
+constexpr int kAttnGroupXSpin = 1 << 22;
+
+__device__ __forceinline__ void attn_group_publish(float amax, AttnGroupX* x, int wave, int round, int lane) {
+  volatile int* tag = x->tag;
+  volatile float* val = x->val[round & 1];
+  if (lane == 0) {
+    val[wave] = amax;
+    tag[wave] = round;
+  }
+}
+
+// The group's maximum of round `round`, once all four waves have published it.
+__device__ __forceinline__ float attn_group_gather(AttnGroupX* x, int round) {
+  volatile int* tag = x->tag;
+  volatile float* val = x->val[round & 1];
+  for (int it = 0; it < kAttnGroupXSpin; ++it) {
+    const int t = __builtin_amdgcn_readfirstlane(min(min(tag[0], tag[1]), min(tag[2], tag[3])));
+    if (t >= round) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return fmaxf(fmaxf(val[0], val[1]), fmaxf(val[2], val[3]));
+}
 
 // Per-workgroup constants of a (b, h, Q tile) work item.  QF: the Q fragments are
 // quantized by the workgroup from 16-bit Q (quant_q) instead of read from q8 / sq.
@@ -188,9 +227,11 @@ struct AttnCtx {
       for (int u = 0; u < 4; ++u) raw[hh][u] = *reinterpret_cast<const uint4*>(qp + 64 * hh + 8 * u);
   }
 
+  // First half of the Q quantizer: f = fp32(q) * c for this lane's 64 values and the wave's
+  // max |f|.
   template <int QDT>
-  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], const AttnQ16& qa, int nq, float* red) {
-    float f[D / 64][32];
+  static __device__ __forceinline__ float quant_q_scaled(const uint4 (&raw)[D / 64][4], float c,
+                                                         float (&f)[D / 64][32]) {
     float amax = 0.0f;
 #pragma unroll
     for (int hh = 0; hh < D / 64; ++hh)
@@ -200,16 +241,18 @@ struct AttnCtx {
         const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          f[hh][8 * u + 2 * i] = Elem<QDT>::lo(w[i]) * qa.c;
-          f[hh][8 * u + 2 * i + 1] = Elem<QDT>::hi(w[i]) * qa.c;
+          f[hh][8 * u + 2 * i] = Elem<QDT>::lo(w[i]) * c;
+          f[hh][8 * u + 2 * i + 1] = Elem<QDT>::hi(w[i]) * c;
           amax = fmaxf(amax, fabsf(f[hh][8 * u + 2 * i]));
           amax = fmaxf(amax, fabsf(f[hh][8 * u + 2 * i + 1]));
         }
       }
-    amax = wave_max(amax);
-    if (lane == 0) red[wave] = amax;
-    attn_barrier();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    return wave_max(amax);
+  }
+
+  // Second half: the block scale from the block maximum, the codes (Q fragments) and, when
+  // qa.sq_out is set, the scale written out.
+  __device__ __forceinline__ void quant_q_codes(const float (&f)[D / 64][32], float amax, const AttnQ16& qa, int nq) {
     const float sc = e4m3_scale(amax);
     const float r = __fdiv_rn(1.0f, sc);
 #pragma unroll
@@ -222,6 +265,17 @@ struct AttnCtx {
                                    clamp448(div_by_scale(f[hh][4 * k + 3], sc, r)));
     sqI = sc;
     if (qa.sq_out != nullptr && wave == 0 && lane == 0) qa.sq_out[(int64_t)bh * nq + I] = sc;
+  }
+
+  // The whole quantizer, the block maximum going through red and a workgroup barrier.
+  template <int QDT>
+  __device__ __forceinline__ void quant_q_raw(const uint4 (&raw)[D / 64][4], const AttnQ16& qa, int nq, float* red) {
+    float f[D / 64][32];
+    float amax = quant_q_scaled<QDT>(raw, qa.c, f);
+    if (lane == 0) red[wave] = amax;
+    attn_barrier();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    quant_q_codes(f, amax, qa, nq);
   }
 
   // Key tile (keys [kv0, kv0 + 128)) -> sK, rows permuted by key_of_row.
@@ -854,9 +908,10 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
 // bit for bit; what goes away is the per-tile copy and barrier and the per-workgroup
 // start-up, which dominate when a Q tile has only a few KV tiles.  QF: Q arrives as 16-bit
 // values and each group quantizes its own 128-row block (quant_q_raw); the block maximum
-// goes through LDS with one workgroup barrier per pair of tiles, which every wave reaches
-// (the loop over pairs is uniform across the workgroup).  No repair path: the launcher uses
-// attn_fwd_kernel for it.
+// goes through LDS among the group's 4 waves (AttnGroupX), one round per pair of tiles that
+// every wave of the group takes part in (the loop over pairs is uniform across the
+// workgroup), so the two groups run independently between head changes.  No repair path:
+// the launcher uses attn_fwd_kernel for it.
 // ---------------------------------------------------------------------------------------
 template <int D>
 struct AttnResident {
@@ -874,10 +929,8 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
   constexpr int NKMAX = AttnResident<D>::NKMAX;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NKMAX * T::BUF];
-  // QF: per-wave block maxima, [pair parity][group][wave]; a pair writes the half its
-  // parity selects, and a wave can only come back to that half after the next pair's
-  // barrier, which every wave reaches after reading this pair's maxima
-  __shared__ float qred[QF ? 16 : 1];
+  // QF: the block-maximum exchange of each group, one round per pair of tiles
+  __shared__ AttnGroupX qgx[QF ? 2 : 1];
   __shared__ __attribute__((aligned(16))) float svl[D];  // the loaded head's channel scales sv
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
@@ -899,6 +952,10 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   v8i qnext[D / 64];
   float sqnext = 0.0f;
   uint4 rawnext[QF ? D / 64 : 1][4];
+  // QF: the next item's scaled Q values (quant_q_scaled), held from the end of one item,
+  // where the group's round for them is published, to the codes at the top of the next
+  float qsc[QF ? D / 64 : 1][QF ? 32 : 1];
+  int round = 0;
   auto fetch_q = [&](int id) {
     const int bh_ = id / nq, I_ = id - bh_ * nq;
     const int row = I_ * 128 + wq * 32 + (lane & 31);
@@ -916,13 +973,16 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       sqnext = sq[(int64_t)bh_ * nq + I_];
     }
   };
-  int parity = 0;
+  if (QF && threadIdx.x < 8) qgx[threadIdx.x >> 2].tag[threadIdx.x & 3] = -1;  // before the first barrier
   int loaded = -1;
   int p = ta;
   if (p < tb) {
     bool act;
     fetch_q(pair_item(p, act));
     wait_vm0();  // so the first pair enters the loop with no load in flight, as later ones do
+    if constexpr (QF)
+      attn_group_publish(AttnCtx<D, HAS_MASK, HAS_BIAS, true>::template quant_q_scaled<ODT>(rawnext, qa.c, qsc),
+                         &qgx[grp], wq, round, lane);
   }
   while (p < tb) {
     const int bh = p / nq;
@@ -948,12 +1008,12 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     AttnCtx<D, HAS_MASK, HAS_BIAS, true> cx(nullptr, k8, v8t, nullptr, sk, key_mask, key_bias, H, Sk, nq, id, wq,
                                             lane);
     if constexpr (QF) {
-      // every wave, active or not, takes part (the barrier inside); a stand-in item
-      // quantizes a real tile and writes no scale
+      // every wave, active or not, takes part in the group's round (published at the end of
+      // the previous item); a stand-in item quantizes a real tile and writes no scale
       AttnQ16 qx = qa;
       if (!active) qx.sq_out = nullptr;
-      cx.template quant_q_raw<ODT>(rawnext, qx, nq, qred + 8 * parity + 4 * grp);
-      parity ^= 1;
+      cx.quant_q_codes(qsc, attn_group_gather(&qgx[grp], round), qx, nq);
+      ++round;
     } else {
 #pragma unroll
       for (int hh = 0; hh < D / 64; ++hh) cx.qf[hh] = qnext[hh];
@@ -967,9 +1027,12 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     if (active) {
       st.init();
       int j = (int)(((int64_t)cx.I * nk) / nq);
-      for (int i = 0; i < nk; ++i) {
+      // One KV tile; LAST: the item's last one, under whose products the next item's Q
+      // loads (written out twice so that the fetched registers are live only there)
+      auto kv_tile = [&](int i, auto last) {
+        constexpr bool LAST = decltype(last)::value;
         // q8 / sq of the next item load under the last tile's products
-        if (!QF && i == nk - 1) fetch_q(nid);
+        if constexpr (!QF && LAST) fetch_q(nid);
         const uint8_t* buf = smem + j * T::BUF;
         const float skj = cx.skh[j];
         const int kv0 = j * 128;
@@ -980,14 +1043,18 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
         // O and l are still zero on the first tile: rescaling them changes no bit
         attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, -1.0f, i > 0, st, pb);
+        // QF: the next item's 16-bit Q rows load under the last tile's PV products, once the
+        // scores and the Q fragments are dead
+        if constexpr (QF && LAST) fetch_q(nid);
         AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
         j = j + 1 == nk ? 0 : j + 1;
-      }
+      };
+      for (int i = 0; i < nk - 1; ++i) kv_tile(i, std::false_type{});
+      kv_tile(nk - 1, std::true_type{});
     }
     // Every path fetches (an inactive group too), so the fetched registers are dead from
-    // their use at the top of the loop to the fetch; QF's 16-bit rows need too many
-    // registers to be in flight during the products.
-    if (QF || !active) fetch_q(nid);
+    // their use at the top of the loop to the fetch.
+    if (!active) fetch_q(nid);
     // nothing but the stores is then in flight at the top of the loop
     wait_vm0();
     if (active && cx.qrow < Sq) {
@@ -995,6 +1062,9 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       svr.load_lds(svl, lane);
       attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
     }
+    // QF: the next item's block maximum, published for the group's round at the top of the loop
+    if constexpr (QF)
+      attn_group_publish(cx.template quant_q_scaled<ODT>(rawnext, qa.c, qsc), &qgx[grp], wq, round, lane);
     p = np;
   }
 }

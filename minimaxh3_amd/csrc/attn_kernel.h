@@ -828,6 +828,59 @@ __device__ __forceinline__ void attn_store(const AttnState<D>& st, const AttnSv<
   }
 }
 
+// attn_store for a wave's whole block of 32 query rows through a 2 KB LDS region of the
+// wave's own (stage): per 32 channels, the lanes write their 8-byte pairs of packed values
+// to the rows they hold, then read back 16 bytes each so that a store instruction writes 16
+// whole 64-byte row segments (non-temporal) instead of 32 rows x 16 bytes.  16-byte chunks
+// are XOR-swizzled by row / 4, so the writes hit each bank at most twice and the reads not
+// at all more than the 16-byte width needs.  wrow0: the block's first row; row_bytes / col_bytes: the row and
+// channel strides in bytes; vec: col_bytes == 2 and wrow0, row_bytes 16-byte aligned (one
+// 16-byte store per chunk; otherwise eight 2-byte stores).  Rows at or past nvalid are not
+// stored.  Same values as attn_store.
+__device__ __forceinline__ int attn_stage_chunk(int row, int c) { return (row * 64) + ((c ^ ((row >> 2) & 3)) << 4); }
+
+template <int D, int ODT>
+__device__ __forceinline__ void attn_store_staged(const AttnState<D>& st, const AttnSv<D>& svr, char* wrow0,
+                                                  int64_t row_bytes, int64_t col_bytes, bool vec, int nvalid,
+                                                  int lane, uint8_t* stage) {
+  constexpr int NDT = D / 32;
+  const int g = lane >> 5;
+  const int q = lane & 31;
+  const float l0 = __shfl(st.lacc[0], q & 15, 64), l1 = __shfl(st.lacc[1], q & 15, 64);
+  const float l = q < 16 ? l0 : l1;
+  const float den = fmaxf(l, 1.0e-12f);
+  const float rden = __fdiv_rn(1.0f, den);
+  // read-back: lane L holds row L / 4 (+ 16), chunk L % 4 of the 64-byte row segment
+  const int rr = lane >> 2, c = lane & 3;
+  char* const dst0 = wrow0 + (int64_t)rr * row_bytes + 8 * c * col_bytes;
+  char* const dst1 = dst0 + 16 * row_bytes;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = div_by_scale(st.o[dt][4 * q4 + e] * svr.r[dt][q4][e], den, rden);
+      *reinterpret_cast<uint2*>(stage + attn_stage_chunk(q, q4) + 8 * g) =
+          make_uint2(cvt_pk_16<ODT>(v[0], v[1]), cvt_pk_16<ODT>(v[2], v[3]));
+    }
+    const v4i a = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr, c));
+    const v4i b = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr + 16, c));
+    if (vec) {
+      // non-temporal: the kernel never reads its output back, and the L2 keeps Q and K/V
+      if (rr < nvalid) __builtin_nontemporal_store(a, reinterpret_cast<v4i*>(dst0 + 64 * dt));
+      if (rr + 16 < nvalid) __builtin_nontemporal_store(b, reinterpret_cast<v4i*>(dst1 + 64 * dt));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t o = (32 * dt + e) * col_bytes;
+        if (rr < nvalid) *reinterpret_cast<uint16_t*>(dst0 + o) = (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
+        if (rr + 16 < nvalid) *reinterpret_cast<uint16_t*>(dst1 + o) = (uint16_t)(b[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // One tile at a time: per KV tile, S = QK^T, codes (and the repair parts), PV.  Two waves
 // per SIMD (256 registers each), so one wave's softmax overlaps the other's products.
@@ -931,6 +984,12 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NKMAX * T::BUF];
   // QF: the block-maximum exchange of each group, one round per pair of tiles
   __shared__ AttnGroupX qgx[QF ? 2 : 1];
+  // 2 KB per wave for the output stores (attn_store_staged), where LDS has room for it
+  constexpr bool STAGE = NKMAX * T::BUF + 8 * 2048 + D * 4 + 2 * (int)sizeof(AttnGroupX) <= 160 * 1024;
+  __shared__ __attribute__((aligned(16))) uint8_t ostage[STAGE ? 8 * 2048 : 16];
+  // whole 16-byte chunks of unit-stride rows
+  const bool ovec = os_d == 1 && ((reinterpret_cast<uintptr_t>(out) | (uintptr_t)(os_b * 2) |
+                                   (uintptr_t)(os_h * 2) | (uintptr_t)(os_s * 2)) & 15u) == 0;
   __shared__ __attribute__((aligned(16))) float svl[D];  // the loaded head's channel scales sv
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
@@ -973,17 +1032,19 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       sqnext = sq[(int64_t)bh_ * nq + I_];
     }
   };
+  auto cx_scaled = [&](const uint4 (&raw)[QF ? D / 64 : 1][4], float (&f)[QF ? D / 64 : 1][QF ? 32 : 1]) {
+    if constexpr (QF) return AttnCtx<D, HAS_MASK, HAS_BIAS, true>::template quant_q_scaled<ODT>(raw, qa.c, f);
+    return 0.0f;
+  };
   if (QF && threadIdx.x < 8) qgx[threadIdx.x >> 2].tag[threadIdx.x & 3] = -1;  // before the first barrier
   int loaded = -1;
   int p = ta;
   if (p < tb) {
     bool act;
+    // in flight with the first head's K/V copies (the head change below waits for both)
     fetch_q(pair_item(p, act));
-    wait_vm0();  // so the first pair enters the loop with no load in flight, as later ones do
-    if constexpr (QF)
-      attn_group_publish(AttnCtx<D, HAS_MASK, HAS_BIAS, true>::template quant_q_scaled<ODT>(rawnext, qa.c, qsc),
-                         &qgx[grp], wq, round, lane);
   }
+  bool first = true;
   while (p < tb) {
     const int bh = p / nq;
     const int seg_end = min(tb, (bh + 1) * nq);
@@ -1003,6 +1064,12 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
       attn_barrier();
       loaded = bh;
     }
+    if constexpr (QF) {
+      // the first item's block maximum (later ones are published at the end of an item)
+      if (first)
+        attn_group_publish(cx_scaled(rawnext, qsc), &qgx[grp], wq, round, lane);
+    }
+    first = false;
     bool active;
     const int id = pair_item(p, active);
     AttnCtx<D, HAS_MASK, HAS_BIAS, true> cx(nullptr, k8, v8t, nullptr, sk, key_mask, key_bias, H, Sk, nq, id, wq,
@@ -1057,14 +1124,21 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     if (!active) fetch_q(nid);
     // nothing but the stores is then in flight at the top of the loop
     wait_vm0();
-    if (active && cx.qrow < Sq) {
+    const int row0 = cx.I * 128 + wq * 32;  // the wave's first query row
+    if (active && row0 < Sq) {
       AttnSv<D> svr;
       svr.load_lds(svl, lane);
-      attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+      if constexpr (STAGE) {
+        char* wrow0 =
+            static_cast<char*>(out) + ((int64_t)cx.b * os_b + (int64_t)cx.h * os_h + (int64_t)row0 * os_s) * 2;
+        attn_store_staged<D, ODT>(st, svr, wrow0, os_s * 2, os_d * 2, ovec, min(32, Sq - row0), lane,
+                                  ostage + 2048 * wave);
+      } else if (cx.qrow < Sq) {
+        attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+      }
     }
     // QF: the next item's block maximum, published for the group's round at the top of the loop
-    if constexpr (QF)
-      attn_group_publish(cx.template quant_q_scaled<ODT>(rawnext, qa.c, qsc), &qgx[grp], wq, round, lane);
+    if constexpr (QF) attn_group_publish(cx_scaled(rawnext, qsc), &qgx[grp], wq, round, lane);
     p = np;
   }
 }

@@ -451,19 +451,38 @@ struct AttnPB {
 
 // Per-tile constants of the code arithmetic (see attn_codes_w4).
 struct AttnCodeK {
-  float c8, cst, c8f, cstf, tau;
+  float c8, cst, c8f, cstf;
+  uint32_t rep_add;  // the repair threshold as a byte addend (attn_repair_addend)
   // cst = 56 - 8 m_new and cstf = (48 - 8 m_new) 2^64 come with the row max (AttnState)
   template <bool HAS_BIAS>
-  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float cst, float cstf, float tau) {
+  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float cst, float cstf, uint32_t rep_add) {
     AttnCodeK k;
     k.cst = cst;
     k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
     k.c8f = k.c8 * 0x1p64f;
     k.cstf = cstf;
-    k.tau = tau;
+    k.rep_add = rep_add;
     return k;
   }
 };
+
+// The repair threshold (kernels/fp8_attention.py:290, P >= tau) on the codes themselves: P is
+// the value of its e4m3 code, and code values grow with the code, so P >= tau exactly when
+// code >= T, T the smallest code whose value is >= tau (127 when none is: codes stay <= 120).
+// Added to a word of four codes (each <= 0x7e), (0x80 - T) per byte sets a byte's top bit
+// exactly when its code is >= T, with no carry between bytes.
+static inline uint32_t attn_repair_addend(float tau) {
+  int T = 127;
+  for (int c = 0; c < 127; ++c) {
+    const int e = c >> 3, m = c & 7;
+    const float v = e == 0 ? m * 0x1p-9f : ldexpf(1.0f + m * 0.125f, e - 7);
+    if (v >= tau) {
+      T = c;
+      break;
+    }
+  }
+  return (uint32_t)(0x80 - T) * 0x01010101u;
+}
 
 // The exp2-free P codes of scores 4 w4 .. 4 w4 + 3 of score subtile t: word 4 (t & 1) + w4
 // of the PV B operand of key half t >> 1.
@@ -516,8 +535,7 @@ __device__ __forceinline__ void attn_codes_w4(const v16f& st, const AttnCodeK& k
       for (int e = 0; e < 4; ++e) {
         // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
         const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
-        const float d = __builtin_fmaf(papx[e], -8.0f, pe8);
-        d8[e] = papx[e] >= k.tau ? d : 0.0f;
+        d8[e] = __builtin_fmaf(papx[e], -8.0f, pe8);
       }
       int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
       hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
@@ -525,8 +543,14 @@ __device__ __forceinline__ void attn_codes_w4(const v16f& st, const AttnCodeK& k
       const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
       int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
       lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
-      pb.hi[t >> 1][4 * (t & 1) + w4] = hi;
-      pb.lo[t >> 1][4 * (t & 1) + w4] = lo;
+      // codes below the threshold take no correction: their hi and lo bytes are cleared.
+      // Byte k of the mask is the top bit of byte k of word + rep_add, spread over the byte
+      // (v_perm's sign-replicating selectors: bytes 1, 3 of the low source and 5, 7 of the
+      // high one, which holds the flags shifted up by a byte)
+      const uint32_t flag = word + k.rep_add;
+      const int mask = (int)__builtin_amdgcn_perm(flag << 8, flag, 0x090b080au);
+      pb.hi[t >> 1][4 * (t & 1) + w4] = hi & mask;
+      pb.lo[t >> 1][4 * (t & 1) + w4] = lo & mask;
     }
   }
 }
@@ -741,7 +765,8 @@ __device__ __forceinline__ bool attn_max_moves(float rmax, float m_old) { return
 // (rescale = false: they are still zero, and scaling them would change no bit), and the
 // tile's codes.  Rows whose max stays take alpha = 1 in a rescale, which changes no bit.
 template <bool HAS_BIAS, bool REP, int D>
-__device__ __forceinline__ void attn_softmax_tile(const v16f (&s)[4], float sq, float skj, float tau, bool rescale,
+__device__ __forceinline__ void attn_softmax_tile(const v16f (&s)[4], float sq, float skj, uint32_t rep_add,
+                                                  bool rescale,
                                                   AttnState<D>& st, AttnPB<REP>& pb) {
   const float rmax = attn_part_max<HAS_BIAS>(s, sq, skj);
   const bool moves = attn_max_moves(rmax, st.m);
@@ -750,7 +775,7 @@ __device__ __forceinline__ void attn_softmax_tile(const v16f (&s)[4], float sq, 
     if (rescale) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
     st.set_m(m_new);
   }
-  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, st.cst, st.cstf, tau);
+  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, st.cst, st.cstf, rep_add);
 #pragma unroll
   for (int t = 0; t < 4; ++t) attn_codes_sub<REP>(s[t], k, t, pb);
 }
@@ -892,7 +917,7 @@ template <int D, bool HAS_MASK, bool HAS_BIAS, bool DO_REPAIR, int ODT, bool QF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8t,
                      const float* __restrict__ sq, const float* __restrict__ sk, const float* __restrict__ sv,
-                     const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, float tau,
+                     const uint8_t* __restrict__ key_mask, const float* __restrict__ key_bias, uint32_t rep_add,
                      void* __restrict__ out, int64_t os_b, int64_t os_h, int64_t os_s, int64_t os_d, int H, int Sq,
                      int Sk, int nq, AttnQ16 qa) {
   typedef AttnTile<D, HAS_MASK || HAS_BIAS> T;
@@ -938,7 +963,7 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-    attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, tau, true, st, pb);
+    attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, rep_add, true, st, pb);
     AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;
   };
@@ -1109,7 +1134,7 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
         // O and l are still zero on the first tile: rescaling them changes no bit
-        attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, -1.0f, i > 0, st, pb);
+        attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, 0u, i > 0, st, pb);
         // QF: the next item's 16-bit Q rows load under the last tile's PV products, once the
         // scores and the Q fragments are dead
         if constexpr (QF && LAST) fetch_q(nid);
@@ -1168,13 +1193,14 @@ static void launch_attn(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8t
     return;
   }
   const dim3 grid((unsigned)(nq * B * H));
+  const uint32_t rep_add = R_ ? attn_repair_addend(tau) : 0u;
   if (qa != nullptr)
     attn_fwd_kernel<D, M_, B_, R_, ODT, true><<<grid, 256, 0, st>>>(
-        nullptr, k8, v8t, nullptr, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk,
+        nullptr, k8, v8t, nullptr, sk, sv, km, kb, rep_add, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk,
         (int)nq, qv);
   else
     attn_fwd_kernel<D, M_, B_, R_, ODT, false><<<grid, 256, 0, st>>>(
-        q8, k8, v8t, sq, sk, sv, km, kb, tau, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
+        q8, k8, v8t, sq, sk, sv, km, kb, rep_add, out, os[0], os[1], os[2], os[3], (int)H, (int)Sq, (int)Sk, (int)nq,
         qv);
 }
 

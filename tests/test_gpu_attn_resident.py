@@ -131,3 +131,29 @@ def test_resident_kv_many_tiles_per_workgroup_mask_bias(D, Sk):
     assert torch.equal(fres.view(torch.int16), res.view(torch.int16))
     assert torch.equal(fstream.view(torch.int16), res.view(torch.int16))
     assert torch.isfinite(res.float()).all()
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_resident_kv_output_channel_stride(D):
+    """A query whose channel stride is not 1 (a [B, D, H, S] tensor viewed as [B, H, S, D]):
+    the output takes the query's strides, so the resident kernel's staged stores write it two
+    bytes at a time.  Bit for bit against the streaming kernel, which writes it element by
+    element, and close to the oracle."""
+    _say(f"attn resident-KV output channel stride D={D}")
+    from minimaxh3_amd import ops
+    B, H, Sq, Sk = 1, 3, 300, 200
+    rng = np.random.default_rng(D + 11)
+    q = bf16_randn(rng, (B, H, Sq, D))
+    k, v = bf16_randn(rng, (B, H, Sk, D)), bf16_randn(rng, (B, H, Sk, D))
+    qg = to_gpu(np.ascontiguousarray(q.transpose(0, 3, 1, 2)), torch.bfloat16).permute(0, 2, 3, 1)
+    assert qg.stride(-1) != 1
+    kg, vg = to_gpu(k, torch.bfloat16), to_gpu(v, torch.bfloat16)
+    c = np.float32(oa.LOG2E / math.sqrt(D))
+    k8, sk = ops.attn_quant_k(kg, ops.attn_kmean(kg))
+    v8t, sv = ops.attn_quant_v(vg)
+    q8, sq = ops.attn_quant_q(qg.contiguous(), float(c))
+    res, stream = _both(lambda m: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, qg, Sk, m))
+    assert res.stride() == qg.stride()
+    assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    ref, _ = oa.fp8_attention(q, k, v, key_mask=None, key_bias=None, repair_tau=-1.0, out_dtype="bf16")
+    assert_attn_close(res.float().cpu().numpy(), ref)

@@ -20,9 +20,9 @@
 // a lane-constant 0/1 selector as A (AttnFragOfs::rowsum_sel).  K and V^T tiles (and the
 // mask / bias of the tile) are copied global -> LDS by the direct-to-LDS DMA.
 //
-// Per score the VALU does half a 3-input max and three FMAs (8 S + 56 - 8 m straight from
-// the fp32 dot product with the per-tile constant 8 sq sk; the flush test as a clamped FMA;
-// rounding to an integer code by adding 1.5 * 2^23), plus three quarters of a byte
+// Per score the VALU does half a 3-input max and three FMAs ((8 S + 56 - 8 m) / 8 straight
+// from the fp32 dot product with the per-tile constant sq sk; the flush test as a clamped
+// FMA; rounding to an integer code by adding 1.5 * 2^20), plus three quarters of a byte
 // permute to pack the codes.  Folding sq * sk into one constant rounds 8 S once instead of
 // twice; the row max that drives the lazy-max policy is still computed exactly as
 // (max * sq) * sk.
@@ -363,12 +363,12 @@ struct AttnState {
   // (see AttnMfmaRun, x == NDT).
   v4f lacc;
   float m;  // lazy row max (log2 domain)
-  // the code constants that depend on m (see attn_codes_w4): 56 - 8 m and (48 - 8 m) 2^64
-  float cst, cstf;
+  // the code constants that depend on m (see attn_codes_w4): 7 - m and (48 - 8 m) 2^64
+  float cst8, cstf;
 
   __device__ __forceinline__ void set_m(float m_new) {
     m = m_new;
-    cst = 56.0f - 8.0f * m_new;
+    cst8 = 7.0f - m_new;
     cstf = (48.0f - 8.0f * m_new) * 0x1p64f;
   }
 
@@ -436,6 +436,16 @@ __device__ __forceinline__ v8i lds_pair(const uint8_t* base, int o0, int o1) {
   return r;
 }
 
+// Four fp32 values divided by 16 -> four e4m3fn bytes (RNE), packed little-endian: the
+// scaled conversion divides by its scale before rounding, so these are the codes of a / 16 ..
+// d / 16 exactly.
+__device__ __forceinline__ int cvt4_e4m3_div16(float a, float b, float c, float d) {
+  typedef short v2s __attribute__((ext_vector_type(2)));
+  const v2s lo = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v2s{0, 0}, a, b, 16.0f, false);
+  const v2s hi = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(lo, c, d, 16.0f, true);
+  return __builtin_bit_cast(int, hi);
+}
+
 // E8M0 block scale of the repair operands: the two e4m3 parts of 8 delta are multiplied
 // by 2^-3 inside the product (127 = 1.0).
 constexpr int kRepairScaleE8M0 = 124;
@@ -451,15 +461,16 @@ struct AttnPB {
 
 // Per-tile constants of the code arithmetic (see attn_codes_w4).
 struct AttnCodeK {
-  float c8, cst, c8f, cstf;
+  float c1, cst8, c8f, cstf;
   uint32_t rep_add;  // the repair threshold as a byte addend (attn_repair_addend)
-  // cst = 56 - 8 m_new and cstf = (48 - 8 m_new) 2^64 come with the row max (AttnState)
+  // cst8 = 7 - m_new and cstf = (48 - 8 m_new) 2^64 come with the row max (AttnState)
   template <bool HAS_BIAS>
-  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float cst, float cstf, uint32_t rep_add) {
+  __device__ __forceinline__ static AttnCodeK make(float sq, float skj, float cst8, float cstf, uint32_t rep_add) {
     AttnCodeK k;
-    k.cst = cst;
-    k.c8 = HAS_BIAS ? 8.0f : (8.0f * sq) * skj;
-    k.c8f = k.c8 * 0x1p64f;
+    k.cst8 = cst8;
+    // sq sk, exactly an eighth of the rounded (8 sq) sk
+    k.c1 = HAS_BIAS ? 1.0f : sq * skj;
+    k.c8f = (k.c1 * 8.0f) * 0x1p64f;
     k.cstf = cstf;
     k.rep_add = rep_add;
     return k;
@@ -489,35 +500,39 @@ static inline uint32_t attn_repair_addend(float tau) {
 //
 // code = bits < 8 ? 0 : rint(bits), bits = 8 S + 56 - 8 m_new.  bits never exceeds
 // 8 * 8 + 56 = 120 (the lazy max keeps S <= m + 8), so the reference's clamp to [0, 126] is
-// inactive.  Three FMAs per score, all at the full FMA rate:
-//   bits = fma(dot, c8, cst)                                 (c8 = 8 sq sk, cst = 56 - 8 m)
-//   keep = clamp01(fma(dot, c8 2^64, (48 - 8 m) 2^64))       (1 when bits >= 8, else 0)
-//   t    = fma(bits, keep, 1.5 * 2^23)
+// inactive.  Three FMAs per score, all at the full FMA rate, on b = bits / 8 (exactly: an
+// eighth of every term, so b = RN(bits) / 8):
+//   b    = fma(dot, c1, cst8)                                (c1 = sq sk, cst8 = 7 - m)
+//   keep = clamp01(fma(dot, 8 c1 2^64, (48 - 8 m) 2^64))     (1 when bits >= 8, else 0)
+//   t    = fma(b, keep, 1.5 * 2^20)
 // keep uses the FMA's free output clamp: the argument is (exact bits - 8) * 2^64, so keep
 // is 0 exactly when bits < 8 (and for invalid keys, whose product overflows to -inf) and
-// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^23 rounds bits to an integer with the
-// FMA's round-to-nearest-even, leaving rint(bits) in the low mantissa bits of t (0 when
-// keep is 0), so v_perm_b32 packs the low bytes of four t's into one dword of codes.
+// 1 once bits exceeds 8 by 2^-64.  Adding 1.5 * 2^20, whose ulp is 2^-3, rounds b to a
+// multiple of 1/8 with the FMA's round-to-nearest-even, i.e. rounds bits to an integer, and
+// leaves rint(bits) in the low mantissa bits of t (0 when keep is 0), so v_perm_b32 packs the
+// low bytes of four t's into one dword of codes.
 //
 // Repair (REP, kernels/fp8_attention.py:288-292): delta = exp2(S - m) - P where P >= tau,
-// else 0.  8 exp2(S - m) = exp2(bits / 8 - 4); P is the decoded code.  delta is bounded by
-// about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and the
-// rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
+// else 0.  exp2(b) = exp2(S - m + 7) = 128 exp2(S - m); P is the decoded code.  delta is
+// bounded by about 11% of exp2(S - m) <= 2^8 (the code's relative error: Mitchell's 6.1% and
+// the rounding of bits), so |8 delta| < 448 and 8 delta splits into e4m3 parts
 // hi = e4m3(8 delta), lo = e4m3(8 delta - hi) (the remainder is exact in fp32), which the
-// PV products multiply with V at the block scale 2^-3.  hi + lo holds 8 delta to about 8
+// PV products multiply with V at the block scale 2^-3.  The conversions take 128 delta and
+// divide it by 16 themselves (v_cvt_scalef32_*: the same codes as plain conversions of
+// 8 delta, and decoded values 16 times theirs).  hi + lo holds 8 delta to about 8
 // significant bits (exactly its bf16 rounding's precision for |8 delta| >= 2^-2; below that
 // lo's e4m3 grid, 2^-9, bounds the error), where the reference rounds delta to bf16.
 template <bool REP>
 __device__ __forceinline__ void attn_codes_w4(const v16f& st, const AttnCodeK& k, int t, int w4, AttnPB<REP>& pb) {
   {
     uint32_t tb[4];
-    float bits[4];
+    float b8[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float x = st[4 * w4 + e];
-      bits[e] = __builtin_fmaf(x, k.c8, k.cst);
+      b8[e] = __builtin_fmaf(x, k.c1, k.cst8);
       const float keep = __builtin_amdgcn_fmed3f(__builtin_fmaf(x, k.c8f, k.cstf), 0.0f, 1.0f);
-      tb[e] = __float_as_uint(__builtin_fmaf(bits[e], keep, 12582912.0f));
+      tb[e] = __float_as_uint(__builtin_fmaf(b8[e], keep, 1572864.0f));
     }
     // bytes [t0, t1, 0, 0] | [0, 0, t2, t3]
     const uint32_t word = __builtin_amdgcn_perm(tb[1], tb[0], 0x0c0c0400u) |
@@ -530,19 +545,16 @@ __device__ __forceinline__ void attn_codes_w4(const v16f& st, const AttnCodeK& k
       const v2f p01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
       const v2f p23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
       const float papx[4] = {p01[0], p01[1], p23[0], p23[1]};
-      float d8[4];
+      float d[4];  // 128 delta
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        // invalid keys: bits ~ -1e30, exp2 -> 0 and the code is 0, so delta = 0
-        const float pe8 = __builtin_amdgcn_exp2f(__builtin_fmaf(bits[e], 0.125f, -4.0f));
-        d8[e] = __builtin_fmaf(papx[e], -8.0f, pe8);
+        // invalid keys: b ~ -1e29, exp2 -> 0 and the code is 0, so delta = 0
+        d[e] = __builtin_fmaf(papx[e], -128.0f, __builtin_amdgcn_exp2f(b8[e]));
       }
-      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0], d8[1], 0, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2], d8[3], hi, true);
-      const v2f h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-      const v2f h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[0] - h01[0], d8[1] - h01[1], 0, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(d8[2] - h23[0], d8[3] - h23[1], lo, true);
+      const int hi = cvt4_e4m3_div16(d[0], d[1], d[2], d[3]);
+      const v2f h01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 16.0f, false);
+      const v2f h23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 16.0f, true);
+      const int lo = cvt4_e4m3_div16(d[0] - h01[0], d[1] - h01[1], d[2] - h23[0], d[3] - h23[1]);
       // codes below the threshold take no correction: their hi and lo bytes are cleared.
       // Byte k of the mask is the top bit of byte k of word + rep_add, spread over the byte
       // (v_perm's sign-replicating selectors: bytes 1, 3 of the low source and 5, 7 of the
@@ -659,8 +671,8 @@ struct AttnMfmaRun {
 };
 
 // Score given to invalid keys: finite and so negative that it loses every row max and
-// flushes to code 0.  The code arithmetic multiplies it by c8 = 8 sq sk (or 8 with a bias),
-// so it is chosen to make that product -1e30 (finite: no inf * 0 = NaN downstream); for
+// flushes to code 0.  The flush test multiplies it by c8 = 8 sq sk (or 8 with a bias), so
+// it is chosen to make that product -1e30 (finite: no inf * 0 = NaN downstream); for
 // c8 < 1e-8 it is -1e38 and the product is smaller still.
 template <bool HAS_BIAS>
 __device__ __forceinline__ float attn_invalid_score(float sq, float skj) {
@@ -775,7 +787,7 @@ __device__ __forceinline__ void attn_softmax_tile(const v16f (&s)[4], float sq, 
     if (rescale) st.rescale(__builtin_amdgcn_exp2f(st.m - m_new));
     st.set_m(m_new);
   }
-  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, st.cst, st.cstf, rep_add);
+  const AttnCodeK k = AttnCodeK::make<HAS_BIAS>(sq, skj, st.cst8, st.cstf, rep_add);
 #pragma unroll
   for (int t = 0; t < 4; ++t) attn_codes_sub<REP>(s[t], k, t, pb);
 }

@@ -220,7 +220,11 @@ int mxf8_attn_quant_kv_gemm_stats(const void* k, const int64_t k_strides[4], con
  * Its scratch is a 4 MiB device array inside the library (one copy per GPU, held until the
  * process ends), enough for every B*H <= 1638 at D = 128 (<= 5461 at D = 64); larger shapes
  * are rejected with MXF8_EINVAL before any launch.  Every call on one GPU shares that
- * GPU's copy: calls that overlap on one GPU (other streams or threads) race.  Outputs are
+ * GPU's copy, so calls must not overlap on one GPU.  Outside graph capture the entry point
+ * orders them itself: a call on another stream than the previous call waits for that call's
+ * event (hipStreamWaitEvent on an event created with the first call on the device), and calls
+ * from several threads are serialized.  Calls captured into a HIP graph are not ordered by the
+ * library: replays of such a graph must not overlap other calls on the GPU.  Outputs are
  * those of mxf8_attn_quant_kv bit for bit.
  */
 int mxf8_attn_quant_kv_noalloc(const void* k, const int64_t k_strides[4], const void* v,

@@ -1167,8 +1167,11 @@ extern "C" int mxf8_attn_quant_kv_gemm_stats(const void* k, const int64_t k_stri
 // copy until the process ends.  Host code never uses the array's name as an address: the
 // entry point's first call on a device (that device current) looks up the device's copy
 // with hipGetSymbolAddress and keeps it.  Every call on one GPU shares that GPU's copy, so
-// calls that overlap on one GPU (other streams, other threads) race.  Nothing in it needs
-// clearing: every partial slab and the key mean are written before they are read.
+// two calls must not overlap on one GPU: outside graph capture the entry point orders them
+// itself (a call on another stream than the previous one first waits for that call's event),
+// while calls captured into a graph are ordered only by how the graph's replays are issued.
+// Nothing in the array needs clearing: every partial slab and the key mean are written before
+// they are read.
 // ---------------------------------------------------------------------------------------
 // 4 MiB: enough for every B*H <= 1638 at D = 128 (<= 5461 at D = 64)
 constexpr int64_t kNoAllocScratchBytes = (int64_t)4 << 20;
@@ -1178,9 +1181,18 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_dev[kMaxDevices];
 std::mutex g_scratch_mu;
+// Per device: an event recorded after the last call made outside graph capture, and that
+// call's stream (created with the device's scratch lookup; guarded by g_scratch_mu).
+struct NoAllocOrder {
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+NoAllocOrder g_noalloc_order[kMaxDevices];
 
-// This device's copy of `scratch` (looked up once per device, with the device current).
-int scratch_ptr(const char* what, void** out) {
+// This device's copy of `scratch` (looked up once per device, with the device current; the
+// device's ordering event is created then too).  *dev_out: the current device.
+int scratch_ptr(const char* what, void** out, int* dev_out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return set_error(MXF8_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
@@ -1193,10 +1205,14 @@ int scratch_ptr(const char* what, void** out) {
       e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
       if (e != hipSuccess || p == nullptr)
         return set_error(MXF8_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", what, hipGetErrorString(e));
+      e = hipEventCreateWithFlags(&g_noalloc_order[dev].done, hipEventDisableTiming);
+      if (e != hipSuccess)
+        return set_error(MXF8_ELAUNCH, "%s: hipEventCreateWithFlags failed: %s", what, hipGetErrorString(e));
       g_scratch_dev[dev].store(p, std::memory_order_release);
     }
   }
   *out = p;
+  *dev_out = dev;
   return MXF8_OK;
 }
 }  // namespace
@@ -1216,12 +1232,33 @@ extern "C" int mxf8_attn_quant_kv_noalloc(const void* k, const int64_t k_strides
                      what, (long long)(B * H), (long long)S, (long long)D, (long long)need,
                      (long long)kNoAllocScratchBytes);
   void* ws = nullptr;
-  rc = scratch_ptr(what, &ws);
+  int dev = 0;
+  rc = scratch_ptr(what, &ws, &dev);
   if (rc) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) return set_error(MXF8_ELAUNCH, "%s: hipStreamIsCapturing failed: %s", what, hipGetErrorString(e));
+  const bool ordered = cap == hipStreamCaptureStatusNone;
   const int64_t BH = B * H;
   const int nch = colreduce_chunks(BH, S);  // as mxf8_attn_quant_kv: the same sums, bit for bit
   float* part = static_cast<float*>(ws);
   float* mean_ws = part + 2 * (int64_t)nch * BH * D;
-  return attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
-                            mean ? mean : mean_ws, part, nch, stream);
+  // the wait, the launches and the record stay together, so that calls from several threads
+  // are ordered as well
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  NoAllocOrder& ord = g_noalloc_order[dev];
+  if (ordered && ord.used && ord.last != stream) {
+    e = hipStreamWaitEvent(stream, ord.done, 0);
+    if (e != hipSuccess) return set_error(MXF8_ELAUNCH, "%s: hipStreamWaitEvent failed: %s", what, hipGetErrorString(e));
+  }
+  rc = attn_quant_kv_impl(what, k, k_strides, v, v_strides, dtype, B, H, S, D, k8, sk, v8t, sv,
+                          mean ? mean : mean_ws, part, nch, stream);
+  if (rc) return rc;
+  if (ordered) {
+    e = hipEventRecord(ord.done, stream);
+    if (e != hipSuccess) return set_error(MXF8_ELAUNCH, "%s: hipEventRecord failed: %s", what, hipGetErrorString(e));
+    ord.last = stream;
+    ord.used = true;
+  }
+  return MXF8_OK;
 }

@@ -4,7 +4,7 @@ The entry point has no counterpart in the reference: it serves callers that cann
 device memory, taking its scratch from a device array inside the library instead of a
 workspace argument.  Through the C ABI, two calls in a row (the second on a smaller input,
 so stale scratch contents from the first would show) must give the workspace entry point's
-outputs bit for bit.
+outputs bit for bit, and so must two calls issued back to back on two streams.
 """
 import ctypes
 
@@ -59,6 +59,30 @@ def test_noalloc_equals_workspace_entry_point_twice(first, second):
             if r.dtype == torch.float8_e4m3fn:
                 r, o = r.view(torch.uint8), o.view(torch.uint8)
             assert torch.equal(r, o), (shape, name, "mean=NULL")
+
+
+def test_noalloc_two_streams_back_to_back():
+    """A large call on one stream, then at once a smaller one on another stream, both keeping
+    the key mean in the scratch array: the entry point orders the second after the first (they
+    share the array), so both equal the workspace entry point bit for bit."""
+    from minimaxh3_amd import ops
+    print("[no-alloc] two streams", flush=True)
+    shapes = ((1, 24, 20280, 128), (2, 3, 3000, 128))
+    inputs = [_packed_kv(*shape, seed=41 + i) for i, shape in enumerate(shapes)]
+    refs = [ops.attn_quant_kv(k, v) for k, v in inputs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for st, (k, v) in zip(streams, inputs):
+        with torch.cuda.stream(st):
+            outs.append(_noalloc(k, v, with_mean=False))
+    torch.cuda.synchronize()
+    for shape, ref, got in zip(shapes, refs, outs):
+        for name, r, o in zip(("k8", "sk", "v8t", "sv"), ref[:4], got[:4]):
+            if r.dtype == torch.float8_e4m3fn:
+                r, o = r.view(torch.uint8), o.view(torch.uint8)
+            assert torch.equal(r, o), (shape, name)
 
 
 def test_noalloc_rejects_shapes_beyond_its_scratch():

@@ -149,6 +149,31 @@ def test_attn_fwd_matches_oracle(tau):
     assert cos(out, ref) > 0.9999
 
 
+@pytest.mark.parametrize("tau", [500.0, 1e30])
+def test_attn_fwd_repair_above_every_code_is_plain(tau):
+    """A repair threshold above the largest e4m3 value (448) corrects no P code: the repair
+    kernel clears every hi / lo byte, its extra products add exact zeros, and its output equals
+    the kernel without the repair bit for bit (mask and bias included)."""
+    _say(f"attn fwd repair tau={tau} against no repair")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(21)
+    B, H, Sq, Sk, D = 2, 3, 400, 900, 128
+    q = to_gpu(bf16_randn(rng, (B, H, Sq, D)), torch.bfloat16)
+    k = to_gpu(bf16_randn(rng, (B, H, Sk, D)), torch.bfloat16)
+    v = to_gpu(bf16_randn(rng, (B, H, Sk, D)), torch.bfloat16)
+    mask = np.ones((B, Sk), bool)
+    mask[1, 700:] = False
+    bias = (rng.standard_normal((B, Sk)) * 0.5).astype(np.float32)
+    km, kb = to_gpu(mask.astype(np.uint8), torch.bool), to_gpu(bias, torch.float32)
+    c = ops.softmax_c(None, D)
+    k8, sk, v8t, sv, _ = ops.attn_quant_kv(k, v)
+    for m, b in ((None, None), (km, kb)):
+        plain = ops.attn_fwd_q(q, c, k8, v8t, sk, sv, m, b, -1.0, Sk, 1)
+        rep = ops.attn_fwd_q(q, c, k8, v8t, sk, sv, m, b, float(tau), Sk, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(plain.view(torch.int16), rep.view(torch.int16))
+
+
 def test_attn_fwd_mask_bias_permuted():
     _say("attn fwd mask+bias permuted")
     rng = np.random.default_rng(12)

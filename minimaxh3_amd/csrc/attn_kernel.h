@@ -865,21 +865,28 @@ __device__ __forceinline__ void attn_store(const AttnState<D>& st, const AttnSv<
   }
 }
 
-// attn_store for a wave's whole block of 32 query rows through a 2 KB LDS region of the
-// wave's own (stage): per 32 channels, the lanes write their 8-byte pairs of packed values
-// to the rows they hold, then read back 16 bytes each so that a store instruction writes 16
-// whole 64-byte row segments (non-temporal) instead of 32 rows x 16 bytes.  16-byte chunks
-// are XOR-swizzled by row / 4, so the writes hit each bank at most twice and the reads not
-// at all more than the 16-byte width needs.  wrow0: the block's first row; row_bytes / col_bytes: the row and
-// channel strides in bytes; vec: col_bytes == 2 and wrow0, row_bytes 16-byte aligned (one
-// 16-byte store per chunk; otherwise eight 2-byte stores).  Rows at or past nvalid are not
-// stored.  Same values as attn_store.
+// attn_store for a wave's whole block of 32 query rows, in two steps.  attn_stage_rows goes
+// through a 2 KB LDS region of the wave's own (stage): per 32 channels, the lanes write their
+// 8-byte pairs of packed values to the rows they hold, then read back 16 bytes each, so that
+// attn_write_rows' store instructions write 16 whole 64-byte row segments (non-temporal)
+// instead of 32 rows x 16 bytes.  16-byte chunks are XOR-swizzled by row / 4, so the writes
+// hit each bank at most twice and the reads not at all more than the 16-byte width needs.
+// The staged rows are held in registers between the two steps.  wrow0: the block's first
+// row; row_bytes / col_bytes: the row and channel strides in bytes; vec: col_bytes == 2 and
+// wrow0, row_bytes 16-byte aligned (one 16-byte store per chunk; otherwise eight 2-byte
+// stores).  Rows at or past nvalid are not stored.  Same values as attn_store.
 __device__ __forceinline__ int attn_stage_chunk(int row, int c) { return (row * 64) + ((c ^ ((row >> 2) & 3)) << 4); }
 
+// The staged rows of a wave, 16 bytes per lane and 32-channel slice for rows lane / 4 and
+// lane / 4 + 16.
+template <int D>
+struct AttnStaged {
+  v4i a[D / 32], b[D / 32];
+};
+
 template <int D, int ODT>
-__device__ __forceinline__ void attn_store_staged(const AttnState<D>& st, const AttnSv<D>& svr, char* wrow0,
-                                                  int64_t row_bytes, int64_t col_bytes, bool vec, int nvalid,
-                                                  int lane, uint8_t* stage) {
+__device__ __forceinline__ void attn_stage_rows(const AttnState<D>& st, const AttnSv<D>& svr, int lane,
+                                                uint8_t* stage, AttnStaged<D>& r) {
   constexpr int NDT = D / 32;
   const int g = lane >> 5;
   const int q = lane & 31;
@@ -889,8 +896,6 @@ __device__ __forceinline__ void attn_store_staged(const AttnState<D>& st, const 
   const float rden = __fdiv_rn(1.0f, den);
   // read-back: lane L holds row L / 4 (+ 16), chunk L % 4 of the 64-byte row segment
   const int rr = lane >> 2, c = lane & 3;
-  char* const dst0 = wrow0 + (int64_t)rr * row_bytes + 8 * c * col_bytes;
-  char* const dst1 = dst0 + 16 * row_bytes;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -901,18 +906,31 @@ __device__ __forceinline__ void attn_store_staged(const AttnState<D>& st, const 
       *reinterpret_cast<uint2*>(stage + attn_stage_chunk(q, q4) + 8 * g) =
           make_uint2(cvt_pk_16<ODT>(v[0], v[1]), cvt_pk_16<ODT>(v[2], v[3]));
     }
-    const v4i a = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr, c));
-    const v4i b = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr + 16, c));
+    r.a[dt] = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr, c));
+    r.b[dt] = *reinterpret_cast<const v4i*>(stage + attn_stage_chunk(rr + 16, c));
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void attn_write_rows(const AttnStaged<D>& r, char* wrow0, int64_t row_bytes,
+                                                int64_t col_bytes, bool vec, int nvalid, int lane) {
+  constexpr int NDT = D / 32;
+  const int rr = lane >> 2, c = lane & 3;
+  char* const dst0 = wrow0 + (int64_t)rr * row_bytes + 8 * c * col_bytes;
+  char* const dst1 = dst0 + 16 * row_bytes;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
     if (vec) {
       // non-temporal: the kernel never reads its output back, and the L2 keeps Q and K/V
-      if (rr < nvalid) __builtin_nontemporal_store(a, reinterpret_cast<v4i*>(dst0 + 64 * dt));
-      if (rr + 16 < nvalid) __builtin_nontemporal_store(b, reinterpret_cast<v4i*>(dst1 + 64 * dt));
+      if (rr < nvalid) __builtin_nontemporal_store(r.a[dt], reinterpret_cast<v4i*>(dst0 + 64 * dt));
+      if (rr + 16 < nvalid) __builtin_nontemporal_store(r.b[dt], reinterpret_cast<v4i*>(dst1 + 64 * dt));
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int64_t o = (32 * dt + e) * col_bytes;
-        if (rr < nvalid) *reinterpret_cast<uint16_t*>(dst0 + o) = (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
-        if (rr + 16 < nvalid) *reinterpret_cast<uint16_t*>(dst1 + o) = (uint16_t)(b[e >> 1] >> (16 * (e & 1)));
+        if (rr < nvalid) *reinterpret_cast<uint16_t*>(dst0 + o) = (uint16_t)(r.a[dt][e >> 1] >> (16 * (e & 1)));
+        if (rr + 16 < nvalid)
+          *reinterpret_cast<uint16_t*>(dst1 + o) = (uint16_t)(r.b[dt][e >> 1] >> (16 * (e & 1)));
       }
     }
   }
@@ -1021,7 +1039,7 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NKMAX * T::BUF];
   // QF: the block-maximum exchange of each group, one round per pair of tiles
   __shared__ AttnGroupX qgx[QF ? 2 : 1];
-  // 2 KB per wave for the output stores (attn_store_staged), where LDS has room for it
+  // 2 KB per wave for the output stores (attn_stage_rows), where LDS has room for it
   constexpr bool STAGE = NKMAX * T::BUF + 8 * 2048 + D * 4 + 2 * (int)sizeof(AttnGroupX) <= 160 * 1024;
   __shared__ __attribute__((aligned(16))) uint8_t ostage[STAGE ? 8 * 2048 : 16];
   // whole 16-byte chunks of unit-stride rows
@@ -1159,20 +1177,25 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
     // Every path fetches (an inactive group too), so the fetched registers are dead from
     // their use at the top of the loop to the fetch.
     if (!active) fetch_q(nid);
-    // nothing but the stores is then in flight at the top of the loop
-    wait_vm0();
     const int row0 = cx.I * 128 + wq * 32;  // the wave's first query row
     if (active && row0 < Sq) {
       AttnSv<D> svr;
       svr.load_lds(svl, lane);
       if constexpr (STAGE) {
+        // the next item's Q loads land while the rows are staged; after the wait nothing but
+        // the stores is in flight at the top of the loop
+        AttnStaged<D> rows;
+        attn_stage_rows<D, ODT>(st, svr, lane, ostage + 2048 * wave, rows);
+        wait_vm0();
         char* wrow0 =
             static_cast<char*>(out) + ((int64_t)cx.b * os_b + (int64_t)cx.h * os_h + (int64_t)row0 * os_s) * 2;
-        attn_store_staged<D, ODT>(st, svr, wrow0, os_s * 2, os_d * 2, ovec, min(32, Sq - row0), lane,
-                                  ostage + 2048 * wave);
-      } else if (cx.qrow < Sq) {
-        attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
+        attn_write_rows<D>(rows, wrow0, os_s * 2, os_d * 2, ovec, min(32, Sq - row0), lane);
+      } else {
+        wait_vm0();
+        if (cx.qrow < Sq) attn_store<D, ODT>(st, svr, cx.b, cx.h, cx.qrow, lane, out, os_b, os_h, os_s, os_d);
       }
+    } else {
+      wait_vm0();
     }
     // QF: the next item's block maximum, published for the group's round at the top of the loop
     if constexpr (QF) attn_group_publish(cx_scaled(rawnext, qsc), &qgx[grp], wq, round, lane);

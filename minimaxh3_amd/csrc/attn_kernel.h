@@ -695,6 +695,20 @@ __device__ __forceinline__ bool attn_tile_needs_mask(const uint8_t* sAux, int kv
   }
 }
 
+// Every key of the tile masked out (a key mask and no bias; keys past Sk read as masked):
+// its scores would all take the masked value, which moves no row max, and its codes would
+// all be 0, adding exact zeros to O and l -- so the streaming kernel skips its softmax and
+// PV products.
+template <bool HAS_MASK, bool HAS_BIAS>
+__device__ __forceinline__ bool attn_tile_all_masked(const uint8_t* sAux, int lane) {
+  if constexpr (!HAS_MASK || HAS_BIAS) {
+    return false;
+  } else {
+    const uint32_t w = lane < 32 ? *reinterpret_cast<const uint32_t*>(sAux + 1024 + 4 * lane) : 0u;
+    return __builtin_amdgcn_ballot_w64(w != 0u) == 0;
+  }
+}
+
 // S = (dot * sq) * sk + bias * log2(e) with every operation rounded on its own, as the
 // reference's statements are (kernels/fp8_attention.py:253, 259).  Contraction is off here:
 // an FMA that one kernel forms and another does not would move S by an ulp, which decides
@@ -991,8 +1005,14 @@ void attn_fwd_kernel(const uint8_t* __restrict__ q8, const uint8_t* __restrict__
     v16f s[4];
     AttnPB<DO_REPAIR> pb;
     AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
-    if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
+    if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane)) {
+      // (tested here, where only tiles with a masked key pay for it)
+      if (attn_tile_all_masked<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, lane)) {
+        j = jn;
+        return;
+      }
       attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
+    }
     attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, rep_add, true, st, pb);
     AttnMfmaRun<D, 0, 2, 0, 0>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
     j = jn;

@@ -82,6 +82,42 @@ def test_resident_kv_equals_streaming_kernel(B, H, Sq, Sk, D, dtype, use_mask, u
     assert_attn_close(res.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_streaming_kernel_skips_fully_masked_tiles(D):
+    """Whole 128-key tiles masked out (the first, a middle and the last one, and every tile of
+    one batch item): the streaming kernel skips their products, which would only have added
+    zeros, so it must equal the resident kernel (which computes every tile) bit for bit; the
+    item with no valid key gives zeros."""
+    _say(f"attn fully masked tiles D={D}")
+    from minimaxh3_amd import ops
+    B, H, Sq, Sk = 3, 2, 300, 512
+    rng = np.random.default_rng(31 + D)
+    q = bf16_randn(rng, (B, H, Sq, D))
+    k, v = bf16_randn(rng, (B, H, Sk, D)), bf16_randn(rng, (B, H, Sk, D))
+    mask = np.ones((B, Sk), bool)
+    mask[0, 128:256] = False
+    mask[0, rng.choice(Sk, 40, replace=False)] = False
+    mask[1, :128] = False
+    mask[1, 384:] = False
+    mask[1, 300:310] = False
+    mask[2, :] = False
+    qg = to_gpu(np.ascontiguousarray(q.transpose(0, 2, 1, 3))).permute(0, 2, 1, 3)
+    kg, vg = to_gpu(k), to_gpu(v)
+    km = to_gpu(mask.astype(np.uint8), torch.bool)
+    c = np.float32(oa.LOG2E / math.sqrt(D))
+    k8, sk = ops.attn_quant_k(kg, ops.attn_kmean(kg))
+    v8t, sv = ops.attn_quant_v(vg)
+    q8, sq = ops.attn_quant_q(qg, float(c))
+    res, stream = _both(lambda m: ops.attn_fwd(q8, k8, v8t, sq, sk, sv, km, None, -1.0, qg, Sk, m))
+    assert torch.equal(res.view(torch.int16), stream.view(torch.int16))
+    fres, fstream = _both(lambda m: ops.attn_fwd_q(qg, float(c), k8, v8t, sk, sv, km, None, -1.0, Sk, m))
+    assert torch.equal(fstream.view(torch.int16), res.view(torch.int16))
+    assert torch.equal(fres.view(torch.int16), res.view(torch.int16))
+    assert not res[2].any()
+    ref, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=None, repair_tau=-1.0, out_dtype="bf16")
+    assert_attn_close(res[:2].float().cpu().numpy(), ref[:2])
+
+
 def test_resident_kv_text_cross_attention_full_size():
     """The joint workload's text cross-attention (B=2, H=24, Sq=21304, Sk=512): both kernels,
     with Q from q8 / sq and with Q quantized inside the launch, give the same bits at full

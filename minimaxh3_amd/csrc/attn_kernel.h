@@ -1070,8 +1070,11 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
   const int grp = wave >> 2, wq = wave & 3, lane = threadIdx.x & 63;
   const int nk = (Sk + 127) / 128;
   const AttnFragOfs<D> fo(lane);
-  const int ta = (int)(((int64_t)blockIdx.x * total) / gridDim.x);
-  const int tb = (int)(((int64_t)(blockIdx.x + 1) * total) / gridDim.x);
+  // XCD-contiguous ranges: the workgroups that share a head's K/V copies mostly sit on one
+  // XCD, whose L2 then fetches them once
+  const int L = xcd_linear_id(blockIdx.x, gridDim.x);
+  const int ta = (int)(((int64_t)L * total) / gridDim.x);
+  const int tb = (int)(((int64_t)(L + 1) * total) / gridDim.x);
   // Work item of this wave's group in the pair that starts at tile p: active when that
   // tile exists (p + grp < end of p's head segment), else a stand-in id.
   auto pair_item = [&](int p, bool& active) {

@@ -697,8 +697,8 @@ __device__ __forceinline__ bool attn_tile_needs_mask(const uint8_t* sAux, int kv
 
 // Every key of the tile masked out (a key mask and no bias; keys past Sk read as masked):
 // its scores would all take the masked value, which moves no row max, and its codes would
-// all be 0, adding exact zeros to O and l -- so the streaming kernel skips its softmax and
-// PV products.
+// all be 0, adding exact zeros to O and l -- so the kernels skip its softmax and PV
+// products.
 template <bool HAS_MASK, bool HAS_BIAS>
 __device__ __forceinline__ bool attn_tile_all_masked(const uint8_t* sAux, int lane) {
   if constexpr (!HAS_MASK || HAS_BIAS) {
@@ -1184,9 +1184,16 @@ void attn_fwd_resident_kernel(const uint8_t* __restrict__ q8, const uint8_t* __r
         v16f s[4];
         AttnPB<false> pb;
         AttnMfmaRun<D, 0, 0, 0, 4>::run(buf + T::KB, buf, fo, pb, cx.qf, s, st);
-        if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane))
+        if (attn_tile_needs_mask<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, kv0, Sk, lane)) {
+          // (not on the last tile, under which the next item's Q rows load: the fetched
+          // registers live across the branch would not fit)
+          if (!LAST && attn_tile_all_masked<HAS_MASK, HAS_BIAS>(buf + T::KB + T::VB, lane)) {
+            j = j + 1 == nk ? 0 : j + 1;
+            return;
+          }
           attn_mask_scores<HAS_MASK, HAS_BIAS>(s, buf + T::KB + T::VB, kv0, Sk, cx.sqI, skj, lane);
-        // O and l are still zero on the first tile: rescaling them changes no bit
+        }
+        // O and l are still zero on the first tile processed: rescaling them changes no bit
         attn_softmax_tile<HAS_BIAS>(s, cx.sqI, skj, 0u, i > 0, st, pb);
         // QF: the next item's 16-bit Q rows load under the last tile's PV products, once the
         // scores and the Q fragments are dead

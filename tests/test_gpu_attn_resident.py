@@ -85,9 +85,9 @@ def test_resident_kv_equals_streaming_kernel(B, H, Sq, Sk, D, dtype, use_mask, u
 @pytest.mark.parametrize("D", [128, 64])
 def test_streaming_kernel_skips_fully_masked_tiles(D):
     """Whole 128-key tiles masked out (the first, a middle and the last one, and every tile of
-    one batch item): the streaming kernel skips their products, which would only have added
-    zeros, so it must equal the resident kernel (which computes every tile) bit for bit; the
-    item with no valid key gives zeros."""
+    one batch item): both kernels skip their products, which would only have added zeros (the
+    resident kernel not on an item's last tile), so they must agree bit for bit; the item with
+    no valid key gives zeros."""
     _say(f"attn fully masked tiles D={D}")
     from minimaxh3_amd import ops
     B, H, Sq, Sk = 3, 2, 300, 512

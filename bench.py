@@ -493,9 +493,13 @@ def summarize_trace(directory: str, workload: str = "dit480") -> str:
     return "\n".join(lines)
 
 
-def summarize_counters(directories: list[str]) -> str:
+def summarize_counters(directories: list[str], workload: str = "dit480") -> str:
     """Per part, the mean over its launches of each counter the passes collected, as busy
-    fractions (SQ counters) and calibrated HBM bytes (FETCH_SIZE / WRITE_SIZE)."""
+    fractions (SQ counters) and calibrated HBM bytes (FETCH_SIZE / WRITE_SIZE); workload: the
+    --workload of the profiled runs."""
+    _, tokens, _, attns, _ = WORKLOADS[workload]
+    anames = tuple(a[0] for a in attns)
+    gemm_names = tuple(n for n, _, _, act in linears_of(workload) if act == 0)
     per = {}
     for d in directories:
         rows = _csv_rows(d, "counter_collection.csv")
@@ -509,7 +513,7 @@ def summarize_counters(directories: list[str]) -> str:
             vals[i][r["Counter_Name"]] += float(r["Counter_Value"])
             if r["Counter_Name"] == "SQ_BUSY_CYCLES":
                 durs[i] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])  # ns
-        lab = _labels([(i, n, g) for i, (n, g) in sorted(names.items())])
+        lab = _labels([(i, n, g) for i, (n, g) in sorted(names.items())], tokens or TOKENS, anames, gemm_names)
         for i, part in lab.items():
             for c, v in vals[i].items():
                 per.setdefault(part, {}).setdefault(c, []).append(v)
@@ -532,7 +536,11 @@ def summarize_counters(directories: list[str]) -> str:
               "VALU instr / MFMA instr | HBM read MB | HBM write MB |" +
               (" LDS active | LDS data FIFO full |" if lds_cols else ""),
               "|---|---|---|---|---|---|---|---|---|---|---|" + ("---|---|" if lds_cols else "")]
-    for p in PART_ORDER:
+    order = list(PART_ORDER)
+    if len(anames) > 1:
+        order += [f"{base}[{n}]" for n in anames for base in ("attn_quant_kv: colreduce", "attn_quant_kv: fold",
+                                                               "attn_quant_kv: quantize", "attn_fwd")]
+    for p in order:
         if p not in per:
             continue
         busy = m(p, "SQ_BUSY_CYCLES")
@@ -594,7 +602,7 @@ def main() -> int:
         print(summarize_trace(args.summarize_trace, args.workload))
         return 0
     if args.summarize_counters:
-        print(summarize_counters(args.summarize_counters))
+        print(summarize_counters(args.summarize_counters, args.workload))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "

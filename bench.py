@@ -61,10 +61,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over this script's dispatches and
 # scaled by what the counters read for the 1 GiB streaming kernel of
 # hbm_stream_reference() (FETCH_SIZE reports 0.500 of the bytes read, WRITE_SIZE 1.000 of
-# the bytes written): 356661.1 KiB x 2 fetched + 121680.2 KiB written.  The algorithmic
+# the bytes written): 357606.2 KiB x 2 fetched + 121680.7 KiB written.  The algorithmic
 # traffic is 249.2 MB of bf16 Q (quantized inside the launch) and K8/V8T read + 124.6 MB
 # of output written.
-ATTN_TRAFFIC_BYTES = 356661.1 * 1024 * 2 + 121680.2 * 1024
+ATTN_TRAFFIC_BYTES = 357606.2 * 1024 * 2 + 121680.7 * 1024
 TOKENS = 20280                # 13 x 30 x 52
 HIDDEN, MLP = 3072, 12288
 HEADS, HEAD_DIM = 24, 128

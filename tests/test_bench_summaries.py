@@ -95,3 +95,27 @@ def test_summarize_counters_fractions_clock_and_calibration(tmp_path):
     # cycles, clock (4e6 cycles in 2 ms), MFMA, VALU, co-issue, LDS, wait, ratio, read MB, write MB
     assert cells[:7] == ["4.00", "2.00", "50.0%", "60.0%", "20.0%", "5.0%", "40.0%"]
     assert cells[8] == f"{100000 * 1024 * 2 / 1e6:.1f}" and cells[9] == f"{50000 * 1024 / 1e6:.1f}"
+
+
+def test_summarize_counters_per_attention_of_the_joint_workload(tmp_path):
+    """--workload joint: the two attention launches of a step (self, then cross) and their K/V
+    quantizers get rows of their own."""
+    step = [("void mxf8::attn_kv_colreduce_kernel<128>(...)", "1"), ("void mxf8::attn_kv_fold_kernel(...)", "1"),
+            ("void mxf8::attn_quant_kv_kernel<128>(...)", "1"),
+            ("void mxf8::attn_fwd_kernel<128, true, false, false, 0, true>(...)", "1"),
+            ("void mxf8::attn_kv_colreduce_kernel<128>(...)", "1"), ("void mxf8::attn_kv_fold_kernel(...)", "1"),
+            ("void mxf8::attn_quant_kv_kernel<128>(...)", "1"),
+            ("void mxf8::attn_fwd_resident_kernel<128, false, false, 0, true>(...)", "1")]
+    busy = {3: 0.5, 7: 0.25}  # MFMA busy of the self and the cross attention
+    rows = []
+    for i, (name, grid) in enumerate(step):
+        cs = {"SQ_BUSY_CYCLES": 32 * 1.0e6, "SQ_VALU_MFMA_BUSY_CYCLES": busy.get(i, 0.0) * 1024 * 1.0e6}
+        for c, v in cs.items():
+            rows.append({"Dispatch_Id": i, "Kernel_Name": name, "Grid_Size": grid, "Counter_Name": c,
+                         "Counter_Value": v, "Start_Timestamp": 0, "End_Timestamp": 1_000_000})
+    _write(tmp_path / "run_counter_collection.csv", rows)
+    table = bench.summarize_counters([str(tmp_path)], "joint")
+    cell = {line.split("|")[1].strip(): [c.strip() for c in line.split("|")[2:-1]]
+            for line in table.splitlines() if line.startswith("| `")}
+    assert cell["`attn_fwd[self]`"][2] == "50.0%" and cell["`attn_fwd[cross]`"][2] == "25.0%"
+    assert "`attn_quant_kv: quantize[cross]`" in cell and "`attn_fwd`" not in cell

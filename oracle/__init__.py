@@ -3,7 +3,8 @@
 This package restates, in numpy, the arithmetic of the reference's FP8 hot path so
 that the HIP implementation can be checked against it.  It is NOT part of the
 product: only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg
-of ``bench.py`` may import it, and only as the checker / the timed CPU baseline.
+of ``bench.py`` may import it, and only to check results against / as the timed CPU
+baseline.
 The product path (``minimaxh3_amd``) never imports it and has no CPU fallback.
 
 Modules

@@ -176,7 +176,7 @@ def test_tau_zero_is_exact_softmax(with_mask, with_bias):
 
 
 def test_fp8_path_close_to_exact_softmax():
-    # tau = -1 (no repair): the north-star accuracy bar against exact attention.
+    # tau = -1 (no repair): the attention accuracy bar (cosine >= 0.999) against exact attention.
     rng = np.random.default_rng(3)
     B, H, S, D = 1, 2, 400, 128
     q, k, v = (_bf16_randn(rng, (B, H, S, D)) for _ in range(3))

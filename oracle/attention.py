@@ -20,6 +20,7 @@ import math
 
 import numpy as np
 
+from .mfma import mfma_f8_dot
 from .numerics import E4M3_MAX, absmax_maxnum, bf16_round, clamp448_maxnum, e4m3_decode, e4m3_encode
 
 F32 = np.float32
@@ -105,7 +106,7 @@ def p_codes(s, m, valid):
 
 
 def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-1.0,
-             block_n=128, q_tiles=None):
+             block_n=128, q_tiles=None, qk_dot="exact"):
     """_fp8_attn_kernel (fp8_attention.py:215-297), fp32 result [B,H,Sq,D].
 
     Per (b, h, Q tile I of 128 rows): m=-1e9, l=0, acc=acc_r=0 (236-239); KV tiles of
@@ -118,8 +119,12 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
     acc += P V (284-286); with repair_tau >= 0 the exact exp2(S - m) minus P is added
     where P >= tau, through bf16 (288-292).  Epilogue: (acc + acc_r) * sV / max(l, 1e-12).
     ``q_tiles`` restricts the work to those 128-row Q tiles (rows of other tiles stay 0);
-    tiles are independent, so this is exact for the rows it computes.
+    tiles are independent, so this is exact for the rows it computes.  ``qk_dot`` "exact"
+    forms Q8 K8^T exactly (rounded once to fp32); "mfma" as the gfx950 fp8 matrix
+    instruction accumulates it (oracle.mfma), which the reference leaves to the hardware.
     """
+    if qk_dot not in ("exact", "mfma"):
+        raise ValueError(f"attn_fwd: qk_dot must be 'exact' or 'mfma', got {qk_dot!r}")
     B, H, Sq, D = q8.shape
     Sk = k8.shape[2]
     nq = _cdiv(Sq, BLOCK_M)
@@ -153,7 +158,10 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
                 cols = j[:, None] * block_n + np.arange(block_n)[None, :]  # [nq, BN]
                 mask_n = cols < Sk
                 Kt = Kd[cols]                                              # [nq, BN, D]
-                s = np.matmul(Qd, Kt.transpose(0, 2, 1)).astype(F32)
+                if qk_dot == "exact":
+                    s = np.matmul(Qd, Kt.transpose(0, 2, 1)).astype(F32)
+                else:
+                    s = mfma_f8_dot(Qd, Kt)
                 skj = np.asarray(sk[b, h], F32)[(j * block_n) // 128][:, None, None]
                 s = ((s * sqI).astype(F32) * skj).astype(F32)
                 valid = mask_m[:, :, None] & mask_n[:, None, :]
@@ -194,11 +202,12 @@ def attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=None, key_bias=None, repair_tau=-
 
 
 def fp8_attention(q, k, v, scale=None, key_mask=None, key_bias=None, repair_tau=-1.0,
-                  out_dtype="bf16", mu=None):
+                  out_dtype="bf16", mu=None, qk_dot="exact"):
     """fp8_attention (fp8_attention.py:300-403) on [B,H,S,D] arrays of input values.
 
     Returns (out [B,H,Sq,D] rounded to bf16 (or fp16), intermediates dict).
-    ``mu`` replaces the key mean when given (the GPU reduction order is not fixed).
+    ``mu`` replaces the key mean when given (the GPU reduction order is not fixed);
+    ``qk_dot`` as in attn_fwd.
     """
     q = np.asarray(q, F32)
     k = np.asarray(k, F32)
@@ -210,7 +219,7 @@ def fp8_attention(q, k, v, scale=None, key_mask=None, key_bias=None, repair_tau=
         mu = key_mean(k)
     k8, sk = quantize_k(k, mu)
     v8t, sv = quantize_v(v)
-    o = attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau)
+    o = attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, qk_dot=qk_dot)
     if out_dtype == "bf16":
         o = bf16_round(o)
     elif out_dtype == "fp16":

@@ -1,0 +1,79 @@
+"""Writes mfma_f8_dot.npz: operands and results of the gfx950 fp8 matrix instruction.
+
+Builds mfma_f8_dot_probe.hip with hipcc into a temporary directory, runs it on cuda:0
+and stores A, B (64 x 128 e4m3 codes each) and the fp32 results C1 (k < 64, one
+instruction) and C2 (all 128 k, two chained instructions), C[i][j] = A[i] . B[j].
+The operands mix the full e4m3 range (subnormals, zeros, both signs), a narrow exponent
+band whose products never lose bits, and rows / columns whose leading products cancel
+inside a group of 8, so that truncation below the group's largest product shows.
+
+    python tests/golden/make_mfma_f8_dot.py [out.npz]
+"""
+import ctypes
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+NAN_CODES = (0x7F, 0xFF)
+
+
+def operands(seed=20261202):
+    rng = np.random.default_rng(seed)
+    full = np.array([c for c in range(256) if c not in NAN_CODES], np.uint8)
+
+    def band(shape, e_lo, e_hi):
+        e = rng.integers(e_lo, e_hi + 1, shape)
+        m = np.where(e == 15, rng.integers(0, 7, shape), rng.integers(0, 8, shape))  # e 15, m 7 is NaN
+        s = rng.integers(0, 2, shape)
+        return ((s << 7) | (e << 3) | m).astype(np.uint8)
+
+    a = np.empty((64, 128), np.uint8)
+    b = np.empty((64, 128), np.uint8)
+    a[:32] = rng.choice(full, (32, 128))
+    b[:32] = rng.choice(full, (32, 128))
+    a[32:48] = band((16, 128), 6, 9)
+    b[32:48] = band((16, 128), 6, 9)
+    # cancelling leaders: per group of 8, A holds the same large code at the group's first
+    # two positions and B holds one large code there with opposite signs
+    a[48:] = band((16, 128), 1, 6)
+    b[48:] = band((16, 128), 1, 6)
+    for g in range(16):
+        big_a = band((16,), 12, 15) & 0x7F
+        big_b = band((16,), 12, 15) & 0x7F
+        a[48:, 8 * g] = big_a
+        a[48:, 8 * g + 1] = big_a
+        b[48:, 8 * g] = big_b
+        b[48:, 8 * g + 1] = big_b | 0x80
+    return a, b
+
+
+def main(out_path):
+    import torch
+
+    a, b = operands()
+    with tempfile.TemporaryDirectory() as tmp:
+        lib_path = os.path.join(tmp, "libmfma_f8_dot_probe.so")
+        subprocess.run(["hipcc", "--offload-arch=gfx950", "-O3", "-shared", "-fPIC", "-Xclang", "-target-feature",
+                        "-Xclang", "-packed-fp32-ops", os.path.join(HERE, "mfma_f8_dot_probe.hip"), "-o", lib_path],
+                       check=True)
+        lib = ctypes.CDLL(lib_path)
+        ag = torch.from_numpy(a).cuda()
+        bg = torch.from_numpy(b).cuda()
+        c1 = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+        c2 = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+        rc = lib.mfma_f8_dot_probe_run(ctypes.c_void_p(ag.data_ptr()), ctypes.c_void_p(bg.data_ptr()),
+                                       ctypes.c_void_p(c1.data_ptr()), ctypes.c_void_p(c2.data_ptr()))
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed: {rc}")
+        np.savez(out_path, a=a, b=b, c1=c1.cpu().numpy(), c2=c2.cpu().numpy(),
+                 device=np.array(torch.cuda.get_device_name(0)))
+    print(f"wrote {out_path}", flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else os.path.join(HERE, "mfma_f8_dot.npz"))

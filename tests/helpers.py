@@ -52,6 +52,30 @@ def assert_attn_close(out, ref, cos_min=0.999, max_abs=2e-2):
     assert c >= cos_min and m <= max_abs, (c, m)
 
 
+def assert_attn_ulps(out, ref, out_dtype, tau):
+    """Bar against the oracle run with the instruction's Q K^T accumulation (qk_dot="mfma"),
+    which fixes every P code the kernel forms: where |ref| >= 2^-6 the outputs lie within
+    1 unit in the last place of the output type (bf16 or fp16), 2 with the repair (tau >= 0);
+    smaller values within 2^-13 absolute (2^-11 with the repair).  What is left is the
+    accumulation of P V and of the row sums on the same instruction and, with the repair,
+    its two e4m3 parts where the reference rounds the correction to bf16."""
+    out = np.asarray(out, np.float32)
+    ref = np.asarray(ref, np.float32)
+    ulps, small_abs = (2, 2.0 ** -11) if tau >= 0 else (1, 2.0 ** -13)
+    if out_dtype == "bf16":
+        to_int = lambda x: (x.view(np.uint32) >> 16).astype(np.int64)  # exact: both are bf16 values
+    else:
+        to_int = lambda x: x.astype(np.float16).view(np.uint16).astype(np.int64)
+    big = np.abs(ref) >= 2.0 ** -6
+    sign_ok = np.signbit(out) == np.signbit(ref)
+    dist = np.abs(to_int(out) - to_int(ref))
+    bad_big = big & (~sign_ok | (dist > ulps))
+    err = np.abs(out.astype(np.float64) - ref)
+    bad_small = ~big & (err > small_abs)
+    assert not bad_big.any(), ("ulps", int(bad_big.sum()), dist[bad_big][:5], out[bad_big][:5], ref[bad_big][:5])
+    assert not bad_small.any(), ("small", int(bad_small.sum()), err[bad_small].max())
+
+
 def assert_ln_close(y, ref, what):
     """LayerNorm output bar: equal almost everywhere; elsewhere within 1 bf16 ulp, or within
     2^-17 absolute where n (1 + scale) and shift cancel (the result's ulp is then far below

@@ -13,7 +13,7 @@ import torch
 
 from oracle import attention as oa
 from oracle.numerics import bf16_round
-from tests.helpers import assert_attn_close, bf16_randn, codes, cos, to_gpu
+from tests.helpers import assert_attn_close, assert_attn_ulps, bf16_randn, codes, cos, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -114,13 +114,15 @@ def test_attention_quant_kv_matches_separate_and_oracle(B, H, S, D, layout, dtyp
     assert not codes(v8t)[..., S:].any()
 
 
-def _fwd_case(rng, B, H, Sq, Sk, D, mask=None, bias=None, tau=-1.0, permuted=False, dtype=torch.bfloat16):
-    """Runs the GPU forward on the oracle's own codes/scales and compares outputs."""
+def _fwd_case(rng, B, H, Sq, Sk, D, mask=None, bias=None, tau=-1.0, permuted=False, dtype=torch.bfloat16,
+              qk_dot="exact"):
+    """Runs the GPU forward on the oracle's own codes/scales; returns it with the oracle's
+    output (Q K^T formed as ``qk_dot`` says, see oracle.attention.attn_fwd)."""
     from minimaxh3_amd import ops
     q, = (bf16_randn(rng, (B, H, Sq, D)),)
     k, v = bf16_randn(rng, (B, H, Sk, D)), bf16_randn(rng, (B, H, Sk, D))
     ref, inter = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=tau,
-                                  out_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
+                                  out_dtype="bf16" if dtype == torch.bfloat16 else "fp16", qk_dot=qk_dot)
     nq, nk = -(-Sq // 128), -(-Sk // 128)
 
     def pad(a, axis, n):
@@ -147,6 +149,10 @@ def test_attn_fwd_matches_oracle(tau):
     out, ref = _fwd_case(rng, 2, 2, 300, 700, 128, tau=tau)
     assert_attn_close(out, ref)
     assert cos(out, ref) > 0.9999
+    # with the instruction's Q K^T accumulation the oracle fixes every P code: 1-2 ulps
+    out_m, ref_m = _fwd_case(np.random.default_rng(11), 2, 2, 300, 700, 128, tau=tau, qk_dot="mfma")
+    np.testing.assert_array_equal(out_m, out)
+    assert_attn_ulps(out_m, ref_m, "bf16", tau)
 
 
 @pytest.mark.parametrize("tau", [500.0, 1e30])
@@ -311,3 +317,4 @@ def test_attn_fwd_tail_tile_mask_bias(use_mask, use_bias, tau):
         bias[1, :10] = -1e9
     out, ref = _fwd_case(rng, B, 3, S, S, 128, mask=mask, bias=bias, tau=tau, permuted=True)
     assert_attn_close(out, ref)
+

@@ -2,8 +2,12 @@
 
 The fused launch must reproduce mxf8_attn_quant_q followed by mxf8_attn_fwd bit for bit
 (same Q codes and scales, then the same kernel arithmetic), its Q scales must equal the
-oracle's quantize_q (fp8_attention.py:54-77), and its output must meet the attention bar
-against the oracle's forward on the same inputs.
+oracle's quantize_q (fp8_attention.py:54-77), and its output must lie within 1-2 output
+ulps of the oracle's forward computed with the fp8 instruction's Q K^T accumulation
+(oracle.mfma) and, for rows of ordinary sharpness (q_std <= 1), meet the attention bar
+against the exact-product oracle.  In sharply peaked rows a P code whose 8 S + 56 - 8 m
+lies within a few thousandths of a rounding boundary follows the instruction's rounding of
+the dot product, and one such code of a dominant key moves the output by up to 4e-2.
 """
 import math
 import sys
@@ -13,7 +17,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
-from tests.helpers import assert_attn_close, bf16_randn, to_gpu
+from tests.helpers import assert_attn_close, assert_attn_ulps, bf16_randn, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +67,9 @@ CASES = [
     (1, 2, 5, 300, 128, torch.bfloat16, "contig", False, True, -1.0, 1.0),
     (1, 1, 128, 1, 64, torch.bfloat16, "qkv", False, False, 0.0, 1.0),
     (1, 2, 384, 256, 128, torch.bfloat16, "perm", False, False, -1.0, 300.0),
+    # peaked rows over a long key sequence (with a key mask, rows whose few valid keys dominate)
+    (1, 2, 640, 2048, 128, torch.bfloat16, "contig", False, False, -1.0, 4.0),
+    (1, 2, 640, 2048, 128, torch.bfloat16, "qkv", True, False, 0.5, 4.0),
 ]
 
 
@@ -107,9 +114,14 @@ def test_fused_q_equals_two_calls_and_oracle(B, H, Sq, Sk, D, dtype, layout, use
     via_op = ops.attn_fwd_q(qg, float(c), k8, v8t, sk, sv, km, kb, float(tau), Sk)
     assert torch.equal(_bits(via_op), _bits(fused))
 
-    ref, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=tau,
-                              out_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
-    assert_attn_close(fused.float().cpu().numpy(), ref)
+    out_dtype = "bf16" if dtype == torch.bfloat16 else "fp16"
+    got = fused.float().cpu().numpy()
+    ref_mfma, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=tau, out_dtype=out_dtype,
+                                   qk_dot="mfma")
+    assert_attn_ulps(got, ref_mfma, out_dtype, tau)
+    if q_std <= 1.0:
+        ref, _ = oa.fp8_attention(q, k, v, key_mask=mask, key_bias=bias, repair_tau=tau, out_dtype=out_dtype)
+        assert_attn_close(got, ref)
 
 
 def test_fp8_attention_fused_and_two_call_paths_agree():

@@ -31,6 +31,21 @@ def _on(t: torch.Tensor | None, device: torch.device, what: str) -> None:
         raise ValueError(f"{what} must be on {device}, got {t.device}")
 
 
+def _check_kv_codes(k8: torch.Tensor, v8t: torch.Tensor, sk: torch.Tensor, sv: torch.Tensor, B: int, H: int,
+                    Sk: int, D: int, device: torch.device, what: str) -> None:
+    """The kernels address K8 / V8T / sK through Sk alone (ceil(Sk/128)*128 padded keys per
+    head), so the codes must have exactly the layout attn_quant_k / attn_quant_v give for Sk
+    keys: a larger Sk would read past them, a smaller one would misplace every head."""
+    Skp = _cdiv(Sk, 128) * 128
+    want = ((k8, (B, H, Skp, D), E4M3, "k8"), (v8t, (B, H, D, Skp), E4M3, "v8t"),
+            (sk, (B, H, Skp // 128), torch.float32, "sk"), (sv, (B, H, D), torch.float32, "sv"))
+    for t, shape, dtype, name in want:
+        if tuple(t.shape) != shape or t.dtype != dtype or not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be a contiguous {dtype} tensor of shape {shape} for Sk={Sk}, "
+                             f"got {t.dtype} {tuple(t.shape)}")
+        _on(t, device, f"{what}: {name}")
+
+
 def key_operands(key_mask: torch.Tensor | None, key_bias: torch.Tensor | None, B: int, Sk: int,
                  device: torch.device) -> tuple[torch.Tensor | None, torch.Tensor | None]:
     """The kernel's per-key operands: a mask as uint8 [B, Sk] (nonzero = keep, the truth value
@@ -427,6 +442,14 @@ def attn_fwd(q8: torch.Tensor, k8: torch.Tensor, v8t: torch.Tensor, sq: torch.Te
     """
     _prep(q8, "attn_fwd")
     B, H, Sq, D = like.shape
+    nq = _cdiv(Sq, 128)
+    if (tuple(q8.shape) != (B, H, nq * 128, D) or q8.dtype != E4M3 or not q8.is_contiguous()
+            or tuple(sq.shape) != (B, H, nq) or sq.dtype != torch.float32 or not sq.is_contiguous()):
+        raise ValueError(f"attn_fwd: q8 [B,H,{nq * 128},D] e4m3 and sq [B,H,{nq}] fp32 (contiguous) expected for "
+                         f"a query of shape {tuple(like.shape)}, got {tuple(q8.shape)} and {tuple(sq.shape)}")
+    _on(sq, q8.device, "attn_fwd: sq")
+    _on(like, q8.device, "attn_fwd: like")
+    _check_kv_codes(k8, v8t, sk, sv, B, H, Sk, D, q8.device, "attn_fwd")
     out = torch.empty_like(like)
     km, kb = key_operands(key_mask, key_bias, B, Sk, q8.device)
     with torch.cuda.device(q8.device):
@@ -467,6 +490,7 @@ def attn_fwd_q(q: torch.Tensor, c: float, k8: torch.Tensor, v8t: torch.Tensor, s
         q8, sq = attn_quant_q(q, c)
         return attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask, key_bias, repair_tau, q, Sk, kv_mode)
     B, H, Sq, D = q.shape
+    _check_kv_codes(k8, v8t, sk, sv, B, H, Sk, D, q.device, "attn_fwd_q")
     out = torch.empty_like(q)
     km, kb = key_operands(key_mask, key_bias, B, Sk, q.device)
     with torch.cuda.device(q.device):

@@ -318,3 +318,29 @@ def test_attn_fwd_tail_tile_mask_bias(use_mask, use_bias, tau):
     out, ref = _fwd_case(rng, B, 3, S, S, 128, mask=mask, bias=bias, tau=tau, permuted=True)
     assert_attn_close(out, ref)
 
+
+def test_attention_rejects_codes_of_another_length():
+    """K8 / V8T / sK are addressed through Sk alone: codes quantized for another number of
+    keys (or of another dtype or layout) raise ValueError before anything is launched."""
+    _say("attn operand checks")
+    from minimaxh3_amd import ops
+    rng = np.random.default_rng(15)
+    B, H, S, D = 1, 2, 300, 128
+    q, k, v = (to_gpu(bf16_randn(rng, (B, H, S, D))) for _ in range(3))
+    k8, sk = ops.attn_quant_k(k, ops.attn_kmean(k))
+    v8t, sv = ops.attn_quant_v(v)
+    q8, sq = ops.attn_quant_q(q, 0.1)
+    for Sk in (400, 200):  # 512 and 256 padded keys where the codes hold 384
+        with pytest.raises(ValueError, match="k8"):
+            ops.attn_fwd_q(q, 0.1, k8, v8t, sk, sv, None, None, -1.0, Sk)
+        with pytest.raises(ValueError, match="k8"):
+            ops.attn_fwd(q8, k8, v8t, sq, sk, sv, None, None, -1.0, q, Sk)
+    with pytest.raises(ValueError, match="sk"):
+        ops.attn_fwd_q(q, 0.1, k8, v8t, sk.double(), sv, None, None, -1.0, S)
+    with pytest.raises(ValueError, match="v8t"):
+        ops.attn_fwd_q(q, 0.1, k8, v8t.transpose(2, 3), sk, sv, None, None, -1.0, S)
+    with pytest.raises(ValueError, match="q8"):
+        ops.attn_fwd(q8[:, :, :256], k8, v8t, sq, sk, sv, None, None, -1.0, q, S)
+    torch.cuda.synchronize()
+    out = ops.attn_fwd_q(q, 0.1, k8, v8t, sk, sv, None, None, -1.0, S)
+    assert out.shape == q.shape

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import numpy as np
 
+from .mfma import mfma_f8_dot
 from .numerics import E4M3_MAX, absmax_maxnum, bf16_round, clamp448_maxnum, e4m3_decode, e4m3_encode
 
 F32 = np.float32
@@ -42,18 +43,21 @@ def quantize_rows(x):
     return e4m3_encode(clamp448_maxnum(q)), scale.reshape(M, 1)
 
 
-def scaled_mm(x8, w8, sa, sw, bias=None):
+def scaled_mm(x8, w8, sa, sw, bias=None, dot="exact"):
     """Row-wise scaled FP8 GEMM, fp32-exact accumulate (fp8_linear.py:95-102).
 
     out[m, n] = (sum_k dec(x8[m,k]) * dec(w8[n,k])) * sa[m] * sw[n] + bias[n]
     x8 [M,K] codes, w8 [N,K] codes, sa [M] or [M,1], sw [N] or [1,N], bias [N] or None.
     Returns fp32 [M, N] before the bf16 cast (products of e4m3 values are exact in
     fp32; the sum is done in float64, the epilogue order of torch._scaled_mm is not
-    fixed by the reference).
+    fixed by the reference).  ``dot="mfma"`` forms the sum as the gfx950 fp8 matrix
+    instruction accumulates it (oracle.mfma) instead; the epilogue is the same.
     """
+    if dot not in ("exact", "mfma"):
+        raise ValueError(f"scaled_mm: dot must be 'exact' or 'mfma', got {dot!r}")
     a = e4m3_decode(x8).astype(np.float64)
     b = e4m3_decode(w8).astype(np.float64)
-    acc = a @ b.T
+    acc = a @ b.T if dot == "exact" else mfma_f8_dot(a, b).astype(np.float64)
     out = acc * np.asarray(sa, np.float64).reshape(-1, 1) * np.asarray(sw, np.float64).reshape(1, -1)
     if bias is not None:
         out = out + np.asarray(bias, np.float64).reshape(1, -1)

@@ -104,3 +104,19 @@ def test_attention_oracle_takes_the_model_for_the_scores(narrow):
     assert np.array_equal(o_exact, o_model) == narrow
     with pytest.raises(ValueError):
         oa.attn_fwd(q8, k8, v8t, sq, sk, sv, qk_dot="bf16")
+
+
+def test_scaled_mm_takes_the_model_for_the_sum():
+    from oracle import linear as ol
+    rng = np.random.default_rng(9)
+    x8, w8 = _codes(rng, (24, 128), 6, 9), _codes(rng, (40, 128), 6, 9)
+    sa = rng.uniform(0.5, 1.0, 24).astype(np.float32)
+    sw = rng.uniform(0.5, 1.0, 40).astype(np.float32)
+    # narrow-band codes: the model's sums are the exact ones
+    np.testing.assert_array_equal(ol.scaled_mm(x8, w8, sa, sw, dot="mfma"), ol.scaled_mm(x8, w8, sa, sw))
+    x8, w8 = _codes(rng, (24, 128), 0, 15), _codes(rng, (40, 128), 0, 15)
+    a, b = _vals(x8), _vals(w8)
+    want = (mfma_f8_dot(a, b).astype(np.float64) * sa[:, None] * sw[None, :]).astype(np.float32)
+    np.testing.assert_array_equal(ol.scaled_mm(x8, w8, sa, sw, dot="mfma"), want)
+    with pytest.raises(ValueError):
+        ol.scaled_mm(x8, w8, sa, sw, dot="bf16")

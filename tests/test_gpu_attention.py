@@ -265,7 +265,8 @@ def test_router_routes_to_fp8_on_gpu():
 ])
 def test_full_size_sampled_tiles(B, Sq, Sk, H, mask_tail):
     """Full-size GPU runs of the DiT attention shapes; the oracle on sampled Q tiles of
-    sampled heads (Q tiles are independent)."""
+    sampled heads (Q tiles are independent), and on one tile per item with the fp8
+    instruction's Q K^T accumulation at the 1-ulp bar."""
     _say(f"full size B={B} Sq={Sq} Sk={Sk} H={H} mask_tail={mask_tail}")
     from minimaxh3_amd.kernels.fp8_attention import fp8_attention
     from minimaxh3_amd import ops
@@ -295,6 +296,20 @@ def test_full_size_sampled_tiles(B, Sq, Sk, H, mask_tail):
             for t in tiles:
                 r0, r1 = t * 128, min(Sq, t * 128 + 128)
                 assert_attn_close(out[b, h, r0:r1].float().cpu().numpy(), ref[0, 0, r0:r1])
+    # head 0 of every item, middle Q tile: within 1 ulp of the oracle with the instruction's
+    # Q K^T accumulation and the key mean the GPU path used
+    _, _, _, _, mean = ops.attn_quant_kv(k, v)
+    t = (Sq // 128) // 2
+    r0, r1 = t * 128, min(Sq, t * 128 + 128)
+    for b in range(B):
+        qn, kn, vn = (x[b:b + 1, :1].float().cpu().numpy() for x in (q, k, v))
+        q8, sq = oa.quantize_q(qn, ops.softmax_c(None, D))
+        k8, sk = oa.quantize_k(kn, mean[b:b + 1, :1].cpu().numpy().reshape(1, 1, 1, D))
+        v8t, sv = oa.quantize_v(vn)
+        km = None if mask is None else mask[b:b + 1].cpu().numpy()
+        ref = bf16_round(oa.attn_fwd(q8, k8, v8t, sq, sk, sv, key_mask=km, q_tiles=[t], qk_dot="mfma"))
+        _say(f"  item {b}: tile {t} against the instruction-model oracle")
+        assert_attn_ulps(out[b, 0, r0:r1].float().cpu().numpy(), ref[0, 0, r0:r1], "bf16", -1.0)
 
 
 @pytest.mark.parametrize("use_mask,use_bias,tau", [

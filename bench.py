@@ -577,6 +577,64 @@ def summarize_counters(directories: list[str], workload: str = "dit480") -> str:
     return "\n".join(lines)
 
 
+def compare_scaled_mm(torch, dev, workload: str, reps: int = 6, inner: int = 10) -> dict:
+    """The reference's own GEMM call on this GPU against mxf8_gemm_rowwise, same operands.
+
+    kernels/fp8_linear.py:95-102 calls torch._scaled_mm(x8, w8.t(), scale_a=x_scale [M, 1],
+    scale_b=w_scale, bias=bias, out_dtype=bf16); on ROCm that is hipBLASLt's row-wise scaled
+    FP8 GEMM.  For each linear of the workload (activations and weights made and quantized as
+    the bench makes them, GELU off on both sides), the two launches are timed alternately,
+    `inner` launches per HIP event pair, best of `reps` pairs each."""
+    from minimaxh3_amd import ops
+    g = torch.Generator(device=dev).manual_seed(1)
+    tokens = WORKLOADS[workload][1]
+    rows = []
+    for name, k, n, _act in linears_of(workload):
+        x = activations(torch, g, tokens, k, dev, workload not in NO_OUTLIERS)
+        w = (torch.randn((n, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        bias = (torch.randn((n,), device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        x8, sa = ops.quant_rows(x)
+        w8, sw = ops.quant_rows(w)
+        sw_row = sw.view(1, -1)
+        ours = lambda: ops.gemm_rowwise(x8, w8, sa, sw_row, bias, 0, None, None, 0.0)
+        ref_call = lambda: torch._scaled_mm(x8, w8.t(), scale_a=sa, scale_b=sw_row, bias=bias,
+                                            out_dtype=torch.bfloat16)
+        row = {"linear": name, "M": tokens, "N": n, "K": k}
+        try:
+            r = ref_call()
+            r = r[0] if isinstance(r, tuple) else r
+        except Exception as exc:  # the call the reference makes is not available here
+            row["scaled_mm"] = f"unavailable: {type(exc).__name__}: {str(exc)[:160]}"
+            r = None
+        o = ours()
+        torch.cuda.synchronize()
+        best = {"mxf8": float("inf"), "scaled_mm": float("inf")}
+        for _ in range(reps):
+            for key, fn in (("mxf8", ours), ("scaled_mm", ref_call if r is not None else None)):
+                if fn is None:
+                    continue
+                s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s0.record()
+                for _ in range(inner):
+                    fn()
+                s1.record()
+                torch.cuda.synchronize()
+                best[key] = min(best[key], s0.elapsed_time(s1) / inner)
+        flops = gemm_flops(tokens, n, k)
+        for key in best:
+            if best[key] != float("inf"):
+                row[f"{key}_us"] = round(best[key] * 1e3, 1)
+                row[f"{key}_tflops"] = round(flops / (best[key] * 1e-3) / 1e12, 1)
+        if r is not None:
+            row["mxf8_over_scaled_mm"] = round(best["scaled_mm"] / best["mxf8"], 3)
+            diff = (o.float() - r.float()).abs().max().item()
+            row["max_abs_diff_over_max_abs"] = round(diff / max(r.float().abs().max().item(), 1e-30), 6)
+        rows.append(row)
+        log(f"[bench] {row}")
+    return {"compare": "torch._scaled_mm (the reference's call, fp8_linear.py:95-102) vs mxf8_gemm_rowwise",
+            "workload": workload, "device": torch.cuda.get_device_name(dev), "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -597,6 +655,9 @@ def main() -> int:
                     help="print the per-part table of a rocprofv3 --kernel-trace run of this script and exit")
     ap.add_argument("--summarize-counters", metavar="DIR", nargs="+",
                     help="print the per-part counter table of rocprofv3 --pmc runs of this script and exit")
+    ap.add_argument("--compare-scaled-mm", action="store_true",
+                    help="time the reference's torch._scaled_mm call (hipBLASLt) against mxf8_gemm_rowwise on "
+                         "the workload's linears, print one JSON object and exit")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace, args.workload))
@@ -620,6 +681,12 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _native.load()
     _native.require_gfx950(dev)
+    if args.compare_scaled_mm:
+        if not linears_of(args.workload) or not WORKLOADS[args.workload][1]:
+            print(f"--compare-scaled-mm: workload {args.workload} has no linears", file=sys.stderr)
+            return 2
+        print(json.dumps(compare_scaled_mm(torch, dev, args.workload)), flush=True)
+        return 0
     desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]
     specs = linears_of(args.workload)
     fuse_q = not args.separate_q_quant

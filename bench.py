@@ -635,6 +635,56 @@ def compare_scaled_mm(torch, dev, workload: str, reps: int = 6, inner: int = 10)
             "workload": workload, "device": torch.cuda.get_device_name(dev), "rows": rows}
 
 
+def compare_sdpa(torch, dev, workload: str, reps: int = 3, inner: int = 5) -> dict:
+    """The FP8 attention call against torch's bf16 scaled_dot_product_attention on this GPU.
+
+    bf16 SDPA is what the reference's router runs for the cases it does not send to the FP8
+    kernel (kernels/attention_router.py); here it takes the same q, k, v for each unmasked
+    attention of the workload.  fp8_attention is the whole call:
+    K/V quantization and the attention launch.  Alternating, `inner` calls per HIP event pair,
+    best of `reps` pairs each."""
+    import torch.nn.functional as F
+    from minimaxh3_amd.kernels.attention_router import _orig_sdpa
+    from minimaxh3_amd.kernels.fp8_attention import fp8_attention
+    _, _, _, attns, _ = WORKLOADS[workload]
+    _, attn_inputs = build_workload(torch, dev, 0, 0, attns, False, (), True)
+    rows = []
+    for (name, b, sq, sk, tail), (_, q, k, v, mask) in zip(attns, attn_inputs):
+        if mask is not None:
+            # a boolean mask can send SDPA to its math path, which holds the whole B x H x Sq x Sk
+            # score matrix (tens of GB here)
+            rows.append({"attention": name, "B": b, "Sq": sq, "Sk": sk, "masked_tail": tail,
+                         "skipped": "key mask: SDPA's masked path would hold the whole score matrix"})
+            continue
+        fns = {"fp8_attention": lambda: fp8_attention(q, k, v),
+               "sdpa_bf16": lambda: _orig_sdpa(q, k, v)}
+        outs = {key: fn() for key, fn in fns.items()}
+        torch.cuda.synchronize()
+        best = {key: float("inf") for key in fns}
+        for _ in range(reps):
+            for key, fn in fns.items():
+                s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s0.record()
+                for _ in range(inner):
+                    fn()
+                s1.record()
+                torch.cuda.synchronize()
+                best[key] = min(best[key], s0.elapsed_time(s1) / inner)
+        flops = attn_flops(b, HEADS, sq, sk, HEAD_DIM)
+        row = {"attention": name, "B": b, "Sq": sq, "Sk": sk, "masked_tail": tail}
+        for key, ms in best.items():
+            row[f"{key}_ms"] = round(ms, 4)
+            row[f"{key}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        row["sdpa_time_over_fp8"] = round(best["sdpa_bf16"] / best["fp8_attention"], 3)
+        a, r = outs["fp8_attention"].float(), outs["sdpa_bf16"].float()
+        row["cosine"] = round((a * r).sum().item() / max((a.norm() * r.norm()).item(), 1e-30), 6)
+        rows.append(row)
+        log(f"[bench] {row}")
+        del outs
+    return {"compare": "torch bf16 scaled_dot_product_attention vs fp8_attention (whole call)",
+            "workload": workload, "device": torch.cuda.get_device_name(dev), "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -655,6 +705,9 @@ def main() -> int:
                     help="print the per-part table of a rocprofv3 --kernel-trace run of this script and exit")
     ap.add_argument("--summarize-counters", metavar="DIR", nargs="+",
                     help="print the per-part counter table of rocprofv3 --pmc runs of this script and exit")
+    ap.add_argument("--compare-sdpa", action="store_true",
+                    help="time torch's bf16 scaled_dot_product_attention against the FP8 attention call on the "
+                         "workload's attentions, print one JSON object and exit")
     ap.add_argument("--compare-scaled-mm", action="store_true",
                     help="time the reference's torch._scaled_mm call (hipBLASLt) against mxf8_gemm_rowwise on "
                          "the workload's linears, print one JSON object and exit")
@@ -681,6 +734,12 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _native.load()
     _native.require_gfx950(dev)
+    if args.compare_sdpa:
+        if not WORKLOADS[args.workload][3]:
+            print(f"--compare-sdpa: workload {args.workload} has no attention", file=sys.stderr)
+            return 2
+        print(json.dumps(compare_sdpa(torch, dev, args.workload)), flush=True)
+        return 0
     if args.compare_scaled_mm:
         if not linears_of(args.workload) or not WORKLOADS[args.workload][1]:
             print(f"--compare-scaled-mm: workload {args.workload} has no linears", file=sys.stderr)

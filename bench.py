@@ -718,6 +718,15 @@ def main() -> int:
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.workload))
         return 0
+    if args.compare_sdpa and args.compare_scaled_mm:
+        print("--compare-sdpa and --compare-scaled-mm are separate runs", file=sys.stderr)
+        return 2
+    if args.compare_sdpa and not WORKLOADS[args.workload][3]:
+        print(f"--compare-sdpa: workload {args.workload} has no attention", file=sys.stderr)
+        return 2
+    if args.compare_scaled_mm and not WORKLOADS[args.workload][1]:
+        print(f"--compare-scaled-mm: workload {args.workload} has no linears", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the FP8 hot path runs on a single MI355X); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -735,15 +744,9 @@ def main() -> int:
     _native.load()
     _native.require_gfx950(dev)
     if args.compare_sdpa:
-        if not WORKLOADS[args.workload][3]:
-            print(f"--compare-sdpa: workload {args.workload} has no attention", file=sys.stderr)
-            return 2
         print(json.dumps(compare_sdpa(torch, dev, args.workload)), flush=True)
         return 0
     if args.compare_scaled_mm:
-        if not linears_of(args.workload) or not WORKLOADS[args.workload][1]:
-            print(f"--compare-scaled-mm: workload {args.workload} has no linears", file=sys.stderr)
-            return 2
         print(json.dumps(compare_scaled_mm(torch, dev, args.workload)), flush=True)
         return 0
     desc, tokens, lora_rank, attns, adaln = WORKLOADS[args.workload]

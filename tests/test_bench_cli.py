@@ -24,3 +24,14 @@ def test_help_lists_the_workloads_and_switches():
         assert flag in r.stdout
     for workload in ("dit480", "joint", "dit720"):
         assert workload in r.stdout
+
+
+def test_comparison_modes_reject_workloads_without_the_compared_part():
+    r = _run("--compare-sdpa", "--workload", "linear2048")
+    assert r.returncode == 2 and "has no attention" in r.stderr
+    r = _run("--compare-scaled-mm", "--workload", "joint")
+    assert r.returncode == 2 and "has no linears" in r.stderr
+    r = _run("--compare-sdpa", "--compare-scaled-mm")
+    assert r.returncode == 2 and "separate runs" in r.stderr
+    r = _run("--help")
+    assert "--compare-sdpa" in r.stdout and "--compare-scaled-mm" in r.stdout

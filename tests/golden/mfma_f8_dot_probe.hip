@@ -1,6 +1,6 @@
-// Generator of tests/golden/mfma_f8_dot.npz: what v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3,
-// fp32 accumulator) returns for given operands, called as the attention and GEMM kernels call
-// it.  A [64][128] and B [64][128] e4m3 codes; wave (bi, bj) computes the 32x32 block
+// Generator of tests/golden/mfma_f8_dot.npz: what v_mfma_f32_32x32x64_f8f6f4 and
+// v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3, fp32 accumulator) return for given operands, called
+// as the attention and GEMM kernels call them.  A [64][128] and B [64][128] e4m3 codes; wave (bi, bj) computes the 32x32 block
 // C[32 bi + r][32 bj + c] = sum_k A[.][k] B[.][k], once over k < 64 (one instruction from a
 // zero accumulator) and once over all 128 (a second instruction chained on the first).
 // Operand bytes: lane l holds row l % 32 of its block, byte j <-> k = 64 h + 32 (l / 32) + j.
@@ -10,6 +10,7 @@
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(64) mfma_f8_dot_probe(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
                                                         float* __restrict__ c1, float* __restrict__ c2) {
@@ -33,9 +34,30 @@ __global__ void __launch_bounds__(64) mfma_f8_dot_probe(const uint8_t* __restric
   }
 }
 
-// a, b: 64 x 128 codes; c1, c2: 64 x 64 fp32 (device pointers).  Returns the launch status.
-extern "C" int mfma_f8_dot_probe_run(const void* a, const void* b, void* c1, void* c2) {
+// The 16x16x128 form: wave (bi, bj) of a 4 x 4 grid computes C16[16 bi + r][16 bj + c] over all
+// 128 k in one instruction.  Operand bytes: lane l holds row l % 16 of its block, byte j <->
+// k = 32 (l / 16) + j.  Accumulator: value i of lane l is row 4 (l / 16) + i, column l % 16.
+__global__ void __launch_bounds__(64) mfma_f8_dot16_probe(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
+                                                          float* __restrict__ c16) {
+  const int bi = blockIdx.x >> 2, bj = blockIdx.x & 3, l = threadIdx.x;
+  const int ra = 16 * bi + (l & 15), rb = 16 * bj + (l & 15);
+  v8i fa, fb;
+  for (int d = 0; d < 8; ++d) {
+    const int k = 32 * (l >> 4) + 4 * d;
+    fa[d] = *reinterpret_cast<const int*>(a + ra * 128 + k);
+    fb[d] = *reinterpret_cast<const int*>(b + rb * 128 + k);
+  }
+  v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const v4f s = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa, fb, z, 0, 0, 0, 0, 0, 0);
+  for (int i = 0; i < 4; ++i) c16[(16 * bi + 4 * (l >> 4) + i) * 64 + 16 * bj + (l & 15)] = s[i];
+}
+
+// a, b: 64 x 128 codes; c1, c2: 64 x 64 fp32; c16: 64 x 64 fp32 (device pointers).  Returns the
+// launch status.
+extern "C" int mfma_f8_dot_probe_run(const void* a, const void* b, void* c1, void* c2, void* c16) {
   hipLaunchKernelGGL(mfma_f8_dot_probe, dim3(4), dim3(64), 0, 0, (const uint8_t*)a, (const uint8_t*)b, (float*)c1,
                      (float*)c2);
+  hipLaunchKernelGGL(mfma_f8_dot16_probe, dim3(16), dim3(64), 0, 0, (const uint8_t*)a, (const uint8_t*)b,
+                     (float*)c16);
   return (int)hipGetLastError();
 }

@@ -52,20 +52,27 @@ def assert_attn_close(out, ref, cos_min=0.999, max_abs=2e-2):
     assert c >= cos_min and m <= max_abs, (c, m)
 
 
-def assert_attn_ulps(out, ref, out_dtype, tau):
-    """Bar against the oracle run with the instruction's Q K^T accumulation (qk_dot="mfma"),
-    which fixes every P code the kernel forms: where |ref| >= 2^-6 the outputs lie within
-    1 unit in the last place of the output type (bf16 or fp16), 2 with the repair (tau >= 0);
-    smaller values within 2^-13 absolute (2^-11 with the repair).  What is left is the
-    accumulation of P V and of the row sums on the same instruction and, with the repair,
-    its two e4m3 parts where the reference rounds the correction to bf16."""
+def assert_attn_model(out, ref, out_dtype, tau):
+    """Bar against the oracle run with the fp8 instruction's arithmetic (dot="mfma"), which
+    forms Q K^T, P V and the row sums as the kernel's matrix instructions do.  Without the
+    repair (tau < 0) at least 99% of the outputs are bit-identical (all of them on most
+    small cases, 99.96% of a tile over 20280 keys, whose accumulators pass through 318
+    instructions, 99.46% over 77648 keys, 1214 instructions); what differs comes from the
+    hardware exp2 of the rescale and the instruction's order of adding its group sums, whose
+    fp32 effects build up along the chain, and lies within 1 unit in the last place of the output type (bf16 or fp16) where
+    |ref| >= 2^-6, else within 2^-13.  With the repair at least 75% are bit-identical (84% at
+    tau = 0, where every key takes a correction; 96-97% at tau = 0.5) and the rest within
+    2 ulps (2^-11 below 2^-6): the kernel carries each correction as two e4m3 parts where
+    the reference rounds it to bf16."""
     out = np.asarray(out, np.float32)
     ref = np.asarray(ref, np.float32)
-    ulps, small_abs = (2, 2.0 ** -11) if tau >= 0 else (1, 2.0 ** -13)
+    ulps, small_abs, min_same = (2, 2.0 ** -11, 0.75) if tau >= 0 else (1, 2.0 ** -13, 0.99)
     if out_dtype == "bf16":
         to_int = lambda x: (x.view(np.uint32) >> 16).astype(np.int64)  # exact: both are bf16 values
     else:
         to_int = lambda x: x.astype(np.float16).view(np.uint16).astype(np.int64)
+    same = (out == ref).mean()
+    assert same >= min_same, ("bit-identical fraction", same)
     big = np.abs(ref) >= 2.0 ** -6
     sign_ok = np.signbit(out) == np.signbit(ref)
     dist = np.abs(to_int(out) - to_int(ref))

@@ -1,5 +1,5 @@
-"""GPU parity of the FP8 linear path against the oracle (quantizer bit-exact, GEMM 1e-2; within one
-bf16 ulp of the oracle with the fp8 instruction's accumulation)."""
+"""GPU parity of the FP8 linear path against the oracle (quantizer bit-exact, GEMM 1e-2; bit-identical
+to the oracle with the fp8 instruction's accumulation)."""
 import sys
 
 import numpy as np
@@ -126,11 +126,11 @@ def test_gemm_rowwise_matches_oracle(M, N, K, bias):
 
 
 @pytest.mark.parametrize("M,N,K,bias", [(300, 512, 1024, True), (129, 256, 3072, False)])
-def test_gemm_rowwise_within_one_ulp_of_the_instruction_model(M, N, K, bias):
+def test_gemm_rowwise_equals_the_instruction_model(M, N, K, bias):
     """Against the oracle with the fp8 instruction's accumulation (oracle.mfma) every output
-    lies within one bf16 ulp, nearly all bit for bit (what is left: the order in which the
-    instruction adds its group sums and the fp32 epilogue against the oracle's float64
-    one); the exact-product oracle misses that bar."""
+    is bit-identical; against the exact-product oracle outputs near zero (where the group
+    truncation of an outlier channel's products survives the cancellation) miss by more
+    than one bf16 ulp."""
     _say(f"gemm model M={M} N={N} K={K} bias={bias}")
     from minimaxh3_amd import ops
     rng = np.random.default_rng(M * 3 + N + K)
@@ -139,17 +139,12 @@ def test_gemm_rowwise_within_one_ulp_of_the_instruction_model(M, N, K, bias):
                            to_gpu(w8, torch.uint8).view(torch.float8_e4m3fn),
                            to_gpu(sa, torch.float32), to_gpu(sw.reshape(1, -1), torch.float32),
                            None if b is None else to_gpu(b), 0, None, None, 0.0).float().cpu().numpy()
-
-    def within_one_ulp(ref):
-        mag = np.maximum(np.abs(out), np.abs(ref)).astype(np.float64)
-        ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(mag, 2.0 ** -126))).astype(np.int64) - 7)
-        return np.abs(out.astype(np.float64) - ref) <= ulp
-
-    model = bf16_round(ol.scaled_mm(x8, w8, sa, sw, b, dot="mfma"))
-    assert within_one_ulp(model).all()
-    assert (out == model).mean() >= 0.99, (out == model).mean()
+    np.testing.assert_array_equal(out, bf16_round(ol.scaled_mm(x8, w8, sa, sw, b, dot="mfma")))
     exact = bf16_round(ol.scaled_mm(x8, w8, sa, sw, b))
-    assert not within_one_ulp(exact).all()
+    mag = np.maximum(np.abs(out), np.abs(exact)).astype(np.float64)
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(mag, 2.0 ** -126))).astype(np.int64) - 7)
+    assert (np.abs(out.astype(np.float64) - exact) > ulp).any()
+
 
 def test_gemm_rowwise_gelu():
     _say("gemm gelu")

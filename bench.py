@@ -626,7 +626,7 @@ def compare_scaled_mm(torch, dev, workload: str, reps: int = 6, inner: int = 10)
                 row[f"{key}_us"] = round(best[key] * 1e3, 1)
                 row[f"{key}_tflops"] = round(flops / (best[key] * 1e-3) / 1e12, 1)
         if r is not None:
-            row["mxf8_over_scaled_mm"] = round(best["scaled_mm"] / best["mxf8"], 3)
+            row["scaled_mm_time_over_mxf8"] = round(best["scaled_mm"] / best["mxf8"], 3)
             diff = (o.float() - r.float()).abs().max().item()
             row["max_abs_diff_over_max_abs"] = round(diff / max(r.float().abs().max().item(), 1e-30), 6)
         rows.append(row)
@@ -705,6 +705,9 @@ def main() -> int:
                     help="print the per-part table of a rocprofv3 --kernel-trace run of this script and exit")
     ap.add_argument("--summarize-counters", metavar="DIR", nargs="+",
                     help="print the per-part counter table of rocprofv3 --pmc runs of this script and exit")
+    ap.add_argument("--no-reference-call", action="store_true",
+                    help="skip the comparison with the reference's torch._scaled_mm call that follows the timed "
+                         "steps of workloads with plain linears (--no-cpu-baseline skips it too)")
     ap.add_argument("--compare-sdpa", action="store_true",
                     help="time torch's bf16 scaled_dot_product_attention against the FP8 attention call on the "
                          "workload's attentions, print one JSON object and exit")
@@ -926,6 +929,20 @@ def main() -> int:
         "kernels": parts,
         "hbm_stream_reference": stream_ref,
     }
+    if tokens and not lora_rank and not adaln and not args.no_reference_call and not args.no_cpu_baseline:
+        # the reference's own GEMM call on this GPU, timed against this GEMM after the timed
+        # region (it does not enter `value`); not in profiling runs (--no-cpu-baseline), whose
+        # kernel traces _labels reads in dispatch order
+        log("[bench] reference GEMM call")
+        try:
+            cmp = compare_scaled_mm(torch, dev, args.workload, reps=3, inner=5)
+            line["reference_gemm_call"] = {
+                "call": "torch._scaled_mm row-wise + bias (kernels/fp8_linear.py:95-102; hipBLASLt on ROCm)",
+                "scaled_mm_time_over_mxf8": {r["linear"]: r.get("scaled_mm_time_over_mxf8", r.get("scaled_mm"))
+                                             for r in cmp["rows"]},
+            }
+        except Exception as exc:  # a failure here must not cost the bench line
+            line["reference_gemm_call"] = {"error": f"{type(exc).__name__}: {str(exc)[:200]}"}
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline")
         line["cpu_baseline"] = cpu_baseline(gemm_f, attn_f, specs, tokens if args.workload in LINEAR_SETS else 0)

@@ -312,6 +312,32 @@ def test_full_size_sampled_tiles(B, Sq, Sk, H, mask_tail):
         assert_attn_model(out[b, 0, r0:r1].float().cpu().numpy(), ref[0, 0, r0:r1], "bf16", -1.0)
 
 
+def test_full_size_repair_matches_the_instruction_model():
+    """The reference's quality profile (repair tau = 0.5) at the 480p shape, B=1 H=24 S=20280
+    D=128: one Q tile of heads 0 and 23 against the oracle with the fp8 instructions'
+    arithmetic and the key mean the GPU path used (within 2 ulps, mostly bit-identical)."""
+    _say("full size repair tau=0.5 S=20280")
+    from minimaxh3_amd.kernels.fp8_attention import fp8_attention
+    from minimaxh3_amd import ops
+    B, S, H, D, tau = 1, 20280, 24, 128, 0.5
+    g = torch.Generator(device="cuda").manual_seed(3)
+    mk = lambda: torch.randn((B, S, H, D), device="cuda", generator=g).to(torch.bfloat16).permute(0, 2, 1, 3)
+    q, k, v = mk(), mk(), mk()
+    out = fp8_attention(q, k, v, repair_tau=tau)
+    _, _, _, _, mean = ops.attn_quant_kv(k, v)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    t = 40
+    r0, r1 = t * 128, t * 128 + 128
+    for h in (0, H - 1):
+        qn, kn, vn = (x[:, h:h + 1].float().cpu().numpy() for x in (q, k, v))
+        q8, sq = oa.quantize_q(qn, ops.softmax_c(None, D))
+        k8, sk = oa.quantize_k(kn, mean[:, h:h + 1].cpu().numpy().reshape(1, 1, 1, D))
+        v8t, sv = oa.quantize_v(vn)
+        ref = bf16_round(oa.attn_fwd(q8, k8, v8t, sq, sk, sv, repair_tau=tau, q_tiles=[t], dot="mfma"))
+        assert_attn_model(out[0, h, r0:r1].float().cpu().numpy(), ref[0, 0, r0:r1], "bf16", tau)
+
+
 @pytest.mark.parametrize("use_mask,use_bias,tau", [
     (True, False, 0.5), (True, False, -1.0), (False, False, 0.5), (True, False, 0.0), (False, True, -1.0),
     (True, True, 0.5),
